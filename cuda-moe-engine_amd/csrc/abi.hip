@@ -1,0 +1,203 @@
+// extern "C" entry points: argument validation (the checks the reference
+// performs with TORCH_CHECK in src/moe_dispatch/csrc/dispatch.cu:95-129,
+// :160-182, :218-243, :294-313, :378-395), then kernel launches on the
+// caller's stream. Nothing here allocates device memory or synchronises.
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+
+#include "moe_common.h"
+
+namespace moe {
+
+int launch_topk_route(const float*, const float*, int32_t*, int64_t*, float*, int64_t, int, int,
+                      hipStream_t);
+int launch_router_fused(const uint16_t*, const float*, const float*, int32_t*, int64_t*, float*,
+                        float*, int64_t, int, int, int, hipStream_t);
+int64_t dispatch_scratch_bytes(int64_t, int64_t, int64_t);
+int launch_dispatch(const void*, int, const int32_t*, int32_t*, int32_t*, int32_t*, void*,
+                    int32_t*, int32_t*, int64_t, int64_t, int, int, int, bool, hipStream_t);
+int launch_combine(const void*, int, const int32_t*, const float*, void*, int64_t, int64_t, int,
+                   int64_t, hipStream_t);
+int launch_swiglu(const void*, int, const int32_t*, void*, int64_t, int64_t, hipStream_t);
+int launch_grouped_gemm(const uint16_t*, const uint16_t*, uint16_t*, const int32_t*, int64_t,
+                        int64_t, int64_t, int, hipStream_t);
+int launch_gateup_swiglu(const uint16_t*, const uint16_t*, uint16_t*, const int32_t*, int64_t,
+                         int64_t, int64_t, int, hipStream_t);
+
+static thread_local char g_last_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+}
+
+int fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int check_launch(const char* what) {
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(MOE_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+    return MOE_OK;
+}
+
+static bool valid_dtype(int dtype) {
+    return dtype == MOE_DTYPE_F32 || dtype == MOE_DTYPE_F16 || dtype == MOE_DTYPE_BF16;
+}
+
+static int64_t aligned_capacity(int64_t n, int64_t experts, int64_t alignment) {
+    if (alignment == 1) return n;
+    return (n + experts * (alignment - 1) + 1 + alignment - 1) / alignment * alignment;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+int moe_abi_version(void) { return MOE_ABI_VERSION; }
+
+const char* moe_status_string(int status) {
+    switch (status) {
+        case MOE_OK: return "ok";
+        case MOE_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case MOE_ERR_UNSUPPORTED: return "unsupported configuration";
+        case MOE_ERR_CAPACITY: return "exceeds int32 indexing capacity";
+        case MOE_ERR_WORKSPACE: return "workspace too small";
+        case MOE_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+const char* moe_last_error(void) { return g_last_error; }
+
+int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64_t* ids64,
+                   float* weights, int64_t tokens, int64_t experts, int64_t topk, void* stream) {
+    MOE_REQUIRE(tokens >= 0, MOE_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED,
+                "routing supports 1..64 experts (got %lld)", (long long)experts);
+    MOE_REQUIRE(topk >= 1 && topk <= kMaxTopk && topk <= experts, MOE_ERR_UNSUPPORTED,
+                "topk must be in 1..min(experts, 8) (got %lld)", (long long)topk);
+    MOE_REQUIRE(tokens <= INT_MAX / experts, MOE_ERR_CAPACITY, "tokens*experts exceeds int32");
+    if (tokens == 0) return MOE_OK;
+    MOE_REQUIRE(logits && bias && ids32 && weights, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    return launch_topk_route(logits, bias, ids32, ids64, weights, tokens, (int)experts, (int)topk,
+                             static_cast<hipStream_t>(stream));
+}
+
+int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
+                     int64_t* ids64, float* weights, float* logits_out, int64_t tokens,
+                     int64_t hidden, int64_t experts, int64_t topk, void* stream) {
+    MOE_REQUIRE(tokens >= 0, MOE_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
+    MOE_REQUIRE(hidden >= 8 && hidden % 8 == 0 && hidden <= INT_MAX, MOE_ERR_UNSUPPORTED,
+                "fused router needs hidden a positive multiple of 8");
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED,
+                "routing supports 1..64 experts");
+    MOE_REQUIRE(topk >= 1 && topk <= kMaxTopk && topk <= experts, MOE_ERR_UNSUPPORTED,
+                "topk must be in 1..min(experts, 8)");
+    MOE_REQUIRE(tokens <= INT_MAX / experts, MOE_ERR_CAPACITY, "tokens*experts exceeds int32");
+    if (tokens == 0) return MOE_OK;
+    MOE_REQUIRE(x && router_w && bias && ids32 && weights, MOE_ERR_INVALID_ARGUMENT,
+                "null pointer");
+    return launch_router_fused(static_cast<const uint16_t*>(x), router_w, bias, ids32, ids64,
+                               weights, logits_out, tokens, (int)hidden, (int)experts, (int)topk,
+                               static_cast<hipStream_t>(stream));
+}
+
+int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
+    if (tokens < 0 || experts < 1 || experts > kMaxExperts || topk < 1 || topk > kMaxTopk)
+        return -1;
+    return dispatch_scratch_bytes(tokens, experts, topk);
+}
+
+int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                 int32_t* slots, void* packed, int32_t* inverse, void* scratch,
+                 int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                 int64_t topk, int64_t alignment, int64_t packed_rows, int vectorized,
+                 void* stream) {
+    MOE_REQUIRE(valid_dtype(dtype), MOE_ERR_INVALID_ARGUMENT, "only FP32, FP16 and BF16 are supported");
+    MOE_REQUIRE(tokens >= 0 && hidden > 0, MOE_ERR_INVALID_ARGUMENT, "incompatible token dimensions");
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
+    MOE_REQUIRE(topk >= 1 && topk <= kMaxTopk, MOE_ERR_UNSUPPORTED, "topk must be in 1..8");
+    MOE_REQUIRE(alignment >= 1 && alignment <= 128, MOE_ERR_INVALID_ARGUMENT, "alignment must be 1..128");
+    const int64_t n = tokens * topk;
+    const int64_t required = aligned_capacity(n, experts, alignment);
+    MOE_REQUIRE(n <= INT_MAX && hidden <= INT_MAX && required <= INT_MAX, MOE_ERR_CAPACITY,
+                "shape exceeds int32 indexing capacity");
+    MOE_REQUIRE(packed_rows >= required, MOE_ERR_WORKSPACE,
+                "packed workspace has %lld rows, needs %lld", (long long)packed_rows,
+                (long long)required);
+    const int64_t need = dispatch_scratch_bytes(tokens, experts, topk);
+    MOE_REQUIRE(scratch_bytes >= need, MOE_ERR_WORKSPACE, "dispatch scratch has %lld bytes, needs %lld",
+                (long long)scratch_bytes, (long long)need);
+    MOE_REQUIRE(counts && offsets && scratch, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(n == 0 || (x && ids && slots && packed && inverse), MOE_ERR_INVALID_ARGUMENT,
+                "null pointer");
+    return launch_dispatch(x, dtype, ids, counts, offsets, slots, packed, inverse,
+                           static_cast<int32_t*>(scratch), tokens, hidden, (int)experts, (int)topk,
+                           (int)alignment, vectorized != 0, static_cast<hipStream_t>(stream));
+}
+
+int moe_combine(const void* expert_output, int dtype, const int32_t* inverse,
+                const float* weights, void* output, int64_t tokens, int64_t hidden,
+                int64_t topk, int64_t packed_rows, void* stream) {
+    MOE_REQUIRE(valid_dtype(dtype), MOE_ERR_INVALID_ARGUMENT, "unsupported output dtype");
+    MOE_REQUIRE(topk >= 1 && topk <= kMaxTopk, MOE_ERR_UNSUPPORTED, "topk must be in 1..8");
+    MOE_REQUIRE(tokens >= 0 && hidden > 0, MOE_ERR_INVALID_ARGUMENT, "invalid output shape");
+    MOE_REQUIRE(tokens * topk <= INT_MAX && hidden <= INT_MAX && packed_rows <= INT_MAX,
+                MOE_ERR_CAPACITY, "invalid output shape");
+    MOE_REQUIRE(packed_rows >= tokens * topk, MOE_ERR_INVALID_ARGUMENT, "shape/dtype mismatch");
+    if (tokens == 0) return MOE_OK;
+    MOE_REQUIRE(expert_output && inverse && weights && output, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    return launch_combine(expert_output, dtype, inverse, weights, output, tokens, hidden,
+                          (int)topk, packed_rows, static_cast<hipStream_t>(stream));
+}
+
+int moe_swiglu(const void* projection, int dtype, const int32_t* valid_rows, void* output,
+               int64_t rows, int64_t width, void* stream) {
+    MOE_REQUIRE(valid_dtype(dtype), MOE_ERR_INVALID_ARGUMENT, "unsupported dtype");
+    MOE_REQUIRE(rows >= 0 && width >= 0 && rows <= INT_MAX && width <= INT_MAX, MOE_ERR_CAPACITY,
+                "shape exceeds index capacity");
+    if (rows * width == 0) return MOE_OK;
+    MOE_REQUIRE(projection && valid_rows && output, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    return launch_swiglu(projection, dtype, valid_rows, output, rows, width,
+                         static_cast<hipStream_t>(stream));
+}
+
+int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offsets, int64_t rows,
+                     int64_t n, int64_t k, int64_t experts, void* stream) {
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
+    MOE_REQUIRE(rows >= 0 && rows <= INT_MAX, MOE_ERR_CAPACITY, "rows exceed int32");
+    MOE_REQUIRE(n > 0 && k > 0 && n % 8 == 0 && k % 8 == 0, MOE_ERR_UNSUPPORTED,
+                "grouped GEMM dimensions must be positive multiples of 8");
+    if (rows == 0) return MOE_OK;
+    MOE_REQUIRE(a && b && c && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    return launch_grouped_gemm(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+                               static_cast<uint16_t*>(c), offsets, rows, n, k, (int)experts,
+                               static_cast<hipStream_t>(stream));
+}
+
+int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
+                              const int32_t* offsets, int64_t rows, int64_t hidden,
+                              int64_t intermediate, int64_t experts, void* stream) {
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
+    MOE_REQUIRE(rows >= 0 && rows <= INT_MAX, MOE_ERR_CAPACITY, "rows exceed int32");
+    MOE_REQUIRE(hidden > 0 && intermediate > 0 && hidden % 8 == 0 && intermediate % 8 == 0,
+                MOE_ERR_UNSUPPORTED, "grouped GEMM dimensions must be positive multiples of 8");
+    if (rows == 0) return MOE_OK;
+    MOE_REQUIRE(a && gate_up && act && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    return launch_gateup_swiglu(static_cast<const uint16_t*>(a),
+                                static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(act),
+                                offsets, rows, hidden, intermediate, (int)experts,
+                                static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

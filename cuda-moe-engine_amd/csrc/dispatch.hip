@@ -1,0 +1,418 @@
+// Token transport kernels for gfx950: deterministic dispatch (histogram,
+// prefix scan, stable pack with fused padding) and the atomic-free weighted
+// combine. Plus the standalone SwiGLU kept for API parity.
+//
+// Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:13-93 (count, scan,
+// pack, combine), :194-275 (aligned layout and padding), :277-323 (SwiGLU).
+// The reference assigns slots with global atomicAdd, so its slot order varies
+// from run to run; here slots follow the flat assignment order, computed with
+// wavefront ballots and per-chunk counts, and every output is deterministic.
+#include <algorithm>
+
+#include "moe_common.h"
+
+namespace moe {
+
+// ---------------------------------------------------------------------------
+// Stage 1: per-chunk histogram and in-chunk stable rank.
+// A chunk is `chunk_tokens` consecutive tokens (chunk_tokens*K assignments).
+// slots[p] <- rank of p among the chunk's earlier assignments to the same
+// expert; chunk_counts[c][e] <- assignments of chunk c to expert e.
+// ---------------------------------------------------------------------------
+constexpr int kRankThreads = 1024;
+constexpr int kRankWaves = kRankThreads / kWave;
+
+__global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
+    const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
+    int32_t* __restrict__ chunk_counts, int64_t n_assign, int experts, int64_t chunk_assign) {
+    __shared__ int running[kMaxExperts];
+    __shared__ int wave_counts[kRankWaves][kMaxExperts];
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * chunk_assign;
+    const int64_t p1 = min(p0 + chunk_assign, n_assign);
+    if (tid < kMaxExperts) running[tid] = 0;
+    for (int64_t base = p0; base < p1; base += kRankThreads) {
+        for (int i = tid; i < kRankWaves * kMaxExperts; i += kRankThreads)
+            (&wave_counts[0][0])[i] = 0;
+        __syncthreads();
+        const int64_t p = base + tid;
+        const bool valid = p < p1;
+        const int e = valid ? ids[p] : -1;
+        const bool in_range = valid && e >= 0 && e < experts;
+        // Lanes holding the same expert id: intersect 6 bit-plane ballots.
+        uint64_t same = __ballot(in_range);
+#pragma unroll
+        for (int b = 0; b < 6; ++b) {
+            const bool bit = (e >> b) & 1;
+            const uint64_t plane = __ballot(in_range && bit);
+            same &= bit ? plane : ~plane;
+        }
+        const int rank = __popcll(same & lanes_below);
+        if (in_range && rank == 0) wave_counts[wave][e] = __popcll(same);
+        __syncthreads();
+        if (valid) {
+            int s = -1;
+            if (in_range) {
+                s = running[e] + rank;
+                for (int w = 0; w < wave; ++w) s += wave_counts[w][e];
+            }
+            slots[p] = s;
+        }
+        __syncthreads();
+        if (tid < experts) {
+            int add = 0;
+            for (int w = 0; w < kRankWaves; ++w) add += wave_counts[w][tid];
+            running[tid] += add;
+        }
+        __syncthreads();
+    }
+    if (tid < experts) chunk_counts[static_cast<int64_t>(blockIdx.x) * experts + tid] = running[tid];
+}
+
+// ---------------------------------------------------------------------------
+// Stage 2: prefix + pack + padding. A block owns `pack_tokens` tokens of one
+// chunk. It rebuilds, from chunk_counts, the expert totals (-> counts and
+// aligned offsets, written by block 0) and the counts of earlier chunks, turns
+// in-chunk ranks into within-expert slots and destinations, and copies each
+// token row once from x to its K destinations with VB-byte accesses. Blocks
+// e, e+grid, ... also zero the padding rows of expert e.
+// ---------------------------------------------------------------------------
+constexpr int kPackThreads = 256;
+constexpr int kPackMaxAssign = 256;  // pack_tokens * K upper bound
+
+template <int VB> struct VecOf;
+template <> struct VecOf<16> { using T = uint4; };
+template <> struct VecOf<8> { using T = uint2; };
+template <> struct VecOf<4> { using T = uint32_t; };
+template <> struct VecOf<2> { using T = uint16_t; };
+
+template <typename V> __device__ __forceinline__ V zero_vec();
+template <> __device__ __forceinline__ uint4 zero_vec<uint4>() { return make_uint4(0, 0, 0, 0); }
+template <> __device__ __forceinline__ uint2 zero_vec<uint2>() { return make_uint2(0, 0); }
+template <> __device__ __forceinline__ uint32_t zero_vec<uint32_t>() { return 0u; }
+template <> __device__ __forceinline__ uint16_t zero_vec<uint16_t>() { return 0; }
+
+template <int VB>
+__global__ __launch_bounds__(kPackThreads) void pack_kernel(
+    const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
+    const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
+    int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
+    int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2) {
+    using V = typename VecOf<VB>::T;
+    __shared__ int part_all[kPackThreads / kWave][kMaxExperts];
+    __shared__ int part_before[kPackThreads / kWave][kMaxExperts];
+    __shared__ int total[kMaxExperts];
+    __shared__ int before[kMaxExperts];
+    __shared__ int offs[kMaxExperts + 1];
+    __shared__ int64_t dest[kPackMaxAssign];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * pack_tokens;
+    const int my_chunk = static_cast<int>(t0 / chunk_tokens);
+
+    // (a) Column sums of chunk_counts: all chunks, and chunks before mine.
+    //     Thread tid always sees expert tid % experts_pow2 (a divisor of 256).
+    {
+        const int e = tid % experts_pow2;
+        int s_all = 0, s_before = 0;
+        if (e < experts) {
+            for (int c = tid / experts_pow2; c < n_chunks; c += kPackThreads / experts_pow2) {
+                const int v = chunk_counts[static_cast<int64_t>(c) * experts + e];
+                s_all += v;
+                if (c < my_chunk) s_before += v;
+            }
+        }
+        for (int m = experts_pow2; m < kWave; m <<= 1) {
+            s_all += __shfl_xor(s_all, m);
+            s_before += __shfl_xor(s_before, m);
+        }
+        if (lane < experts_pow2 && lane < kMaxExperts) {
+            part_all[wave][lane] = s_all;
+            part_before[wave][lane] = s_before;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int tot = 0, bef = 0;
+        if (lane < experts) {
+            for (int w = 0; w < kPackThreads / kWave; ++w) {
+                tot += part_all[w][lane];
+                bef += part_before[w][lane];
+            }
+        }
+        const int span = (tot + alignment - 1) / alignment * alignment;
+        int incl = span;  // inclusive scan over the wavefront
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int up = __shfl_up(incl, d);
+            if (lane >= d) incl += up;
+        }
+        if (lane < experts) {
+            total[lane] = tot;
+            before[lane] = bef;
+            offs[lane + 1] = incl;
+        }
+        if (lane == 0) offs[0] = 0;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (tid < experts) counts[tid] = total[tid];
+        if (tid <= experts) offsets[tid] = offs[tid];
+    }
+
+    // (b) Destinations of this block's assignments.
+    const int64_t t_end = min(t0 + pack_tokens, tokens);
+    const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
+    const int n_local = n_tok * topk;
+    for (int i = tid; i < n_local; i += kPackThreads) {
+        const int64_t p = t0 * topk + i;
+        const int e = ids[p];
+        int64_t d = -1;
+        if (e >= 0 && e < experts) {
+            const int r = slots[p];
+            if (r >= 0) {
+                const int slot = before[e] + r;
+                d = static_cast<int64_t>(offs[e]) + slot;
+                slots[p] = slot;
+                inverse[p] = static_cast<int32_t>(d);
+            }
+        }
+        dest[i] = d;
+    }
+    __syncthreads();
+
+    // (c) Row copies: each x row is read once and written to its K rows.
+    const int64_t nv = row_bytes / VB;
+    const int64_t items = static_cast<int64_t>(n_tok) * nv;
+    for (int64_t i = tid; i < items; i += kPackThreads) {
+        const int tl = static_cast<int>(i / nv);
+        const int64_t v = i - static_cast<int64_t>(tl) * nv;
+        const V val = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[v];
+        for (int k = 0; k < topk; ++k) {
+            const int64_t d = dest[tl * topk + k];
+            if (d >= 0) reinterpret_cast<V*>(packed + d * row_bytes)[v] = val;
+        }
+    }
+
+    // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
+    for (int e = blockIdx.x; e < experts; e += gridDim.x) {
+        const int64_t r0 = offs[e] + total[e];
+        const int64_t r1 = offs[e + 1];
+        const int64_t pad_items = (r1 - r0) * nv;
+        V* base = reinterpret_cast<V*>(packed + r0 * row_bytes);
+        for (int64_t i = tid; i < pad_items; i += kPackThreads) base[i] = zero_vec<V>();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Combine: out[t] = round(sum_k w[t,k] * y[inverse[t,k]]) in fp32, k order,
+// separate multiply and add (no contraction), skipped rows outside [0, R).
+// One thread per (token, VE-element vector).
+// ---------------------------------------------------------------------------
+template <int DT, int VE>
+__global__ __launch_bounds__(256) void combine_kernel(
+    const typename Elem<DT>::T* __restrict__ y, const int32_t* __restrict__ inverse,
+    const float* __restrict__ weights, typename Elem<DT>::T* __restrict__ out, int64_t tokens,
+    int64_t hidden, int topk, int64_t rows) {
+#pragma clang fp contract(off)
+    using T = typename Elem<DT>::T;
+    struct alignas(sizeof(T) * VE) Pack {
+        T v[VE];
+    };
+    const int64_t nv = hidden / VE;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t t = idx / nv;
+    if (t >= tokens) return;
+    const int64_t v = idx - t * nv;
+    float acc[VE];
+#pragma unroll
+    for (int j = 0; j < VE; ++j) acc[j] = 0.0f;
+    for (int k = 0; k < topk; ++k) {
+        const int64_t p = t * topk + k;
+        const int row = inverse[p];
+        if (row >= 0 && row < rows) {
+            const float w = weights[p];
+            const Pack in = reinterpret_cast<const Pack*>(y + static_cast<int64_t>(row) * hidden)[v];
+#pragma unroll
+            for (int j = 0; j < VE; ++j) {
+                const float prod = w * Elem<DT>::load(in.v[j]);
+                acc[j] = acc[j] + prod;
+            }
+        }
+    }
+    Pack o;
+#pragma unroll
+    for (int j = 0; j < VE; ++j) o.v[j] = Elem<DT>::store(acc[j]);
+    reinterpret_cast<Pack*>(out + t * hidden)[v] = o;
+}
+
+// ---------------------------------------------------------------------------
+// Standalone SwiGLU (API parity; the block fuses it into the gate/up GEMM).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void swiglu_kernel(const typename Elem<DT>::T* __restrict__ proj,
+                                                     const int32_t* __restrict__ valid_rows,
+                                                     typename Elem<DT>::T* __restrict__ out,
+                                                     int64_t rows, int64_t width) {
+    const int64_t elements = rows * width;
+    const int64_t valid = *valid_rows;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < elements;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t r = i / width;
+        const int64_t c = i - r * width;
+        if (r >= valid) {
+            out[i] = Elem<DT>::store(0.0f);
+            continue;
+        }
+        const int64_t base = r * width * 2 + c;
+        const float g = Elem<DT>::load(proj[base]);
+        const float u = Elem<DT>::load(proj[base + width]);
+        out[i] = Elem<DT>::store((g / (1.0f + expf(-g))) * u);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+struct DispatchPlan {
+    int64_t chunk_tokens;
+    int64_t n_chunks;
+    int pack_tokens;
+    int64_t pack_blocks;
+};
+
+static int64_t pow2_at_least(int64_t v) {
+    int64_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// Chunk size keeps n_chunks * E <= 1024 (each pack block rebuilds its prefix
+// from the whole chunk_counts table); pack blocks move about 16 KiB of rows.
+DispatchPlan plan_dispatch(int64_t tokens, int64_t experts, int64_t topk, int64_t row_bytes) {
+    DispatchPlan p{};
+    int64_t chunk = 16;
+    while (chunk < tokens && ((tokens + chunk - 1) / chunk) * experts > 1024) chunk <<= 1;
+    p.chunk_tokens = chunk;
+    p.n_chunks = tokens > 0 ? (tokens + chunk - 1) / chunk : 0;
+    int64_t pt = 1;
+    const int64_t max_pt = kPackMaxAssign / topk;
+    while (pt * 2 <= max_pt && pt * 2 <= chunk && pt * row_bytes < 16384) pt <<= 1;
+    p.pack_tokens = static_cast<int>(pt);
+    p.pack_blocks = tokens > 0 ? (tokens + pt - 1) / pt : 1;
+    return p;
+}
+
+int64_t dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
+    const DispatchPlan p = plan_dispatch(tokens, experts, topk, 16);
+    const int64_t n = p.n_chunks * experts;
+    return (n > 0 ? n : 1) * static_cast<int64_t>(sizeof(int32_t));
+}
+
+int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts,
+                    int32_t* offsets, int32_t* slots, void* packed, int32_t* inverse,
+                    int32_t* chunk_counts, int64_t tokens, int64_t hidden, int experts, int topk,
+                    int alignment, bool vectorized, hipStream_t stream) {
+    const int64_t elem = dtype_size(dtype);
+    const int64_t row_bytes = hidden * elem;
+    const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes);
+    const int64_t n_assign = tokens * topk;
+    if (plan.n_chunks > 0) {
+        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)),
+                           dim3(kRankThreads), 0, stream, ids, slots, chunk_counts, n_assign,
+                           experts, plan.chunk_tokens * topk);
+        int rc = check_launch("count_rank_kernel");
+        if (rc != MOE_OK) return rc;
+    }
+    int vb = static_cast<int>(elem);
+    if (vectorized) {
+        if (row_bytes % 16 == 0) vb = 16;
+        else if (row_bytes % 8 == 0) vb = 8;
+        else if (row_bytes % 4 == 0) vb = 4;
+    }
+    const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
+    const dim3 grid(static_cast<unsigned>(plan.pack_blocks));
+#define MOE_PACK_CASE(VBV)                                                                   \
+    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                \
+                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets, \
+                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,  \
+                       alignment, plan.chunk_tokens, plan.pack_tokens,                        \
+                       static_cast<int>(plan.n_chunks), experts_pow2)
+    switch (vb) {
+        case 16: MOE_PACK_CASE(16); break;
+        case 8: MOE_PACK_CASE(8); break;
+        case 4: MOE_PACK_CASE(4); break;
+        case 2: MOE_PACK_CASE(2); break;
+        default: return fail(MOE_ERR_UNSUPPORTED, "row size %lld bytes", (long long)row_bytes);
+    }
+#undef MOE_PACK_CASE
+    return check_launch("pack_kernel");
+}
+
+template <int DT, int VE>
+static void launch_combine_t(const void* y, const int32_t* inverse, const float* weights,
+                             void* out, int64_t tokens, int64_t hidden, int topk, int64_t rows,
+                             hipStream_t stream) {
+    using T = typename Elem<DT>::T;
+    const int64_t threads = tokens * (hidden / VE);
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    hipLaunchKernelGGL((combine_kernel<DT, VE>), grid, dim3(256), 0, stream,
+                       static_cast<const T*>(y), inverse, weights, static_cast<T*>(out), tokens,
+                       hidden, topk, rows);
+}
+
+int launch_combine(const void* y, int dtype, const int32_t* inverse, const float* weights,
+                   void* out, int64_t tokens, int64_t hidden, int topk, int64_t rows,
+                   hipStream_t stream) {
+    if (tokens == 0) return MOE_OK;
+    switch (dtype) {
+        case MOE_DTYPE_BF16:
+            if (hidden % 8 == 0) launch_combine_t<MOE_DTYPE_BF16, 8>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            else launch_combine_t<MOE_DTYPE_BF16, 1>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            break;
+        case MOE_DTYPE_F16:
+            if (hidden % 8 == 0) launch_combine_t<MOE_DTYPE_F16, 8>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            else launch_combine_t<MOE_DTYPE_F16, 1>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            break;
+        case MOE_DTYPE_F32:
+            if (hidden % 4 == 0) launch_combine_t<MOE_DTYPE_F32, 4>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            else launch_combine_t<MOE_DTYPE_F32, 1>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            break;
+        default: return fail(MOE_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+    }
+    return check_launch("combine_kernel");
+}
+
+int launch_swiglu(const void* proj, int dtype, const int32_t* valid_rows, void* out, int64_t rows,
+                  int64_t width, hipStream_t stream) {
+    const int64_t elements = rows * width;
+    if (elements == 0) return MOE_OK;
+    const int64_t blocks = std::min<int64_t>((elements + 255) / 256, 1 << 20);
+    const dim3 grid(static_cast<unsigned>(blocks));
+    switch (dtype) {
+        case MOE_DTYPE_BF16:
+            hipLaunchKernelGGL(swiglu_kernel<MOE_DTYPE_BF16>, grid, dim3(256), 0, stream,
+                               static_cast<const uint16_t*>(proj), valid_rows,
+                               static_cast<uint16_t*>(out), rows, width);
+            break;
+        case MOE_DTYPE_F16:
+            hipLaunchKernelGGL(swiglu_kernel<MOE_DTYPE_F16>, grid, dim3(256), 0, stream,
+                               static_cast<const uint16_t*>(proj), valid_rows,
+                               static_cast<uint16_t*>(out), rows, width);
+            break;
+        case MOE_DTYPE_F32:
+            hipLaunchKernelGGL(swiglu_kernel<MOE_DTYPE_F32>, grid, dim3(256), 0, stream,
+                               static_cast<const float*>(proj), valid_rows,
+                               static_cast<float*>(out), rows, width);
+            break;
+        default: return fail(MOE_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+    }
+    return check_launch("swiglu_kernel");
+}
+
+}  // namespace moe

@@ -1,0 +1,298 @@
+// Grouped bf16 expert GEMMs on CDNA4 MFMA (v_mfma_f32_32x32x16_bf16).
+//
+// Problem: for every expert e, rows r in [offsets[e], offsets[e+1]) of A
+// [R, K] multiply B[e]^T (B is [E, N, K], K-contiguous like A) into C [R, N].
+// Reference behaviour: src/moe_dispatch/experts.py:21-35 and the persistent
+// Triton kernel src/moe_dispatch/_triton_gemm.py:16-72 (device-resident
+// ENDS = offsets[1:], masked partial row tiles, fp32 accumulation, bf16
+// output). The gate/up variant fuses the SwiGLU of csrc/dispatch.cu:277-292
+// into the epilogue: gate and up columns of the same output column land in the
+// same lane, so the activation is computed in registers.
+//
+// Design (gfx950):
+//  * Block tile BM x BN x 64, 4 wavefronts in a WAVES_M x WAVES_N grid, each
+//    wave owns (BM/WAVES_M) x (BN/WAVES_N) as 32x32 MFMA sub-tiles; the fp32
+//    accumulators live in the AGPR/VGPR file (one wave per SIMD).
+//  * Global -> register -> LDS double buffering with one barrier per k-step.
+//    LDS rows are 128 bytes; 16-byte chunks are XOR-swizzled by (row & 7) so
+//    both the 16-byte stores and the MFMA fragment reads are conflict free.
+//  * Tile schedule is built on the device from offsets: expert e contributes
+//    ceil(span_e/BM) x n_tiles tiles (0 for an empty expert). The grid is a
+//    host-side upper bound; surplus workgroups exit at once.
+//  * XCD-aware order: workgroup i runs on XCD i % 8, so logical tiles are
+//    remapped to give each XCD a contiguous range; inside an expert tiles go
+//    N-major so the row tiles of one expert share each weight slice in L2.
+#include "moe_common.h"
+
+namespace moe {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kBK = 64;  // k-step: one 128-byte LDS row
+
+struct GemmParams {
+    const uint16_t* a;        // [R, K]
+    const uint16_t* b;        // [E, NB, K]  (NB = N, or 2I for gate/up)
+    uint16_t* c;              // [R, ldc]
+    const int32_t* offsets;   // [E + 1]
+    int64_t k;                // reduction length (H or I)
+    int64_t nb;               // rows of one expert's B
+    int64_t n_out;            // output columns (N, or I for gate/up)
+    int64_t ldc;
+    int experts;
+    int n_tiles;              // output column tiles
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
+__global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p) {
+    constexpr int WTM = BM / WAVES_M;
+    constexpr int WTN = BN / WAVES_N;
+    constexpr int SM = WTM / 32;
+    constexpr int SN = WTN / 32;
+    constexpr int A_LOADS = BM * kBK / 8 / kGemmThreads;  // 16-byte chunks per thread
+    constexpr int B_LOADS = BN * kBK / 8 / kGemmThreads;
+    static_assert(WAVES_M * WAVES_N == 4, "4 wavefronts");
+    static_assert(A_LOADS >= 1 && B_LOADS >= 1, "tile too small");
+    static_assert(!SWIGLU || (SN % 2 == 0), "gate/up pairing needs an even sub-tile count");
+
+    __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * kBK];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BN * kBK];
+
+    // ---- tile lookup -------------------------------------------------------
+    const int32_t* __restrict__ offs = p.offsets;
+    int total = 0;
+    for (int e = 0; e < p.experts; ++e) {
+        const int span = offs[e + 1] - offs[e];
+        total += ((span + BM - 1) / BM) * p.n_tiles;
+    }
+    const int per_xcd = (total + kNumXcd - 1) / kNumXcd;
+    const int slot = blockIdx.x / kNumXcd;
+    if (slot >= per_xcd) return;
+    const int tile = (blockIdx.x % kNumXcd) * per_xcd + slot;
+    if (tile >= total) return;
+    int expert = 0, base = 0, m_tiles = 0;
+    for (; expert < p.experts; ++expert) {
+        const int span = offs[expert + 1] - offs[expert];
+        m_tiles = (span + BM - 1) / BM;
+        const int t = m_tiles * p.n_tiles;
+        if (tile < base + t) break;
+        base += t;
+    }
+    const int rel = tile - base;
+    const int n_tile = rel / m_tiles;
+    const int m_tile = rel - n_tile * m_tiles;
+    const int64_t row0 = offs[expert] + static_cast<int64_t>(m_tile) * BM;
+    const int64_t row_end = offs[expert + 1];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WAVES_N;
+    const int wn = wave % WAVES_N;
+
+    // ---- per-thread global chunk pointers ----------------------------------
+    const uint16_t* a_src[A_LOADS];
+    int a_dst[A_LOADS];
+    bool a_ok[A_LOADS];
+    int a_kc[A_LOADS];
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+        const int chunk = tid + i * kGemmThreads;
+        const int r = chunk >> 3, c = chunk & 7;
+        const int64_t grow = row0 + r;
+        a_ok[i] = grow < row_end;
+        a_src[i] = p.a + (a_ok[i] ? grow : row0) * p.k + c * 8;
+        a_dst[i] = swz(r, c);
+        a_kc[i] = c * 8;
+    }
+    const uint16_t* b_src[B_LOADS];
+    int b_dst[B_LOADS];
+    bool b_ok[B_LOADS];
+    int b_kc[B_LOADS];
+    const uint16_t* b_expert = p.b + static_cast<int64_t>(expert) * p.nb * p.k;
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+        const int chunk = tid + i * kGemmThreads;
+        const int r = chunk >> 3, c = chunk & 7;
+        int64_t brow;
+        bool ok;
+        if constexpr (SWIGLU) {
+            // LDS row r -> wave column block r / WTN; first half gate, second half up.
+            const int wcol = r / WTN, w = r % WTN;
+            constexpr int HALF = WTN / 2;
+            const int64_t col = static_cast<int64_t>(n_tile) * (BN / 2) + wcol * HALF + (w % HALF);
+            ok = col < p.n_out;
+            brow = (w < HALF) ? col : p.n_out + col;
+        } else {
+            const int64_t col = static_cast<int64_t>(n_tile) * BN + r;
+            ok = col < p.n_out;
+            brow = col;
+        }
+        b_ok[i] = ok;
+        b_src[i] = b_expert + (ok ? brow : 0) * p.k + c * 8;
+        b_dst[i] = swz(r, c);
+        b_kc[i] = c * 8;
+    }
+
+    floatx16 acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    uint4 ra[A_LOADS], rb[B_LOADS];
+    const int64_t K = p.k;
+    const int k_steps = static_cast<int>((K + kBK - 1) / kBK);
+
+    auto load_tile = [&](int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i)
+            ra[i] = (a_ok[i] && k0 + a_kc[i] < K) ? *reinterpret_cast<const uint4*>(a_src[i] + k0)
+                                                  : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i)
+            rb[i] = (b_ok[i] && k0 + b_kc[i] < K) ? *reinterpret_cast<const uint4*>(b_src[i] + k0)
+                                                  : make_uint4(0, 0, 0, 0);
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) *reinterpret_cast<uint4*>(&lds_a[buf][a_dst[i]]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) *reinterpret_cast<uint4*>(&lds_b[buf][b_dst[i]]) = rb[i];
+    };
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+
+    const int frag_row = lane & 31;
+    const int frag_half = lane >> 5;
+    for (int kt = 0; kt < k_steps; ++kt) {
+        const int buf = kt & 1;
+        const bool has_next = kt + 1 < k_steps;
+        if (has_next) load_tile(static_cast<int64_t>(kt + 1) * kBK);
+        const uint16_t* la = lds_a[buf];
+        const uint16_t* lb = lds_b[buf];
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            const int chunk = kk * 2 + frag_half;
+            bf16x8_t af[SM], bfr[SN];
+#pragma unroll
+            for (int i = 0; i < SM; ++i) {
+                const int r = wm * WTM + i * 32 + frag_row;
+                af[i] = *reinterpret_cast<const bf16x8_t*>(&la[swz(r, chunk)]);
+            }
+#pragma unroll
+            for (int j = 0; j < SN; ++j) {
+                const int r = wn * WTN + j * 32 + frag_row;
+                bfr[j] = *reinterpret_cast<const bf16x8_t*>(&lb[swz(r, chunk)]);
+            }
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int j = 0; j < SN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (has_next) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue ------------------------------------------------------------
+    // Accumulator register r of a 32x32 sub-tile holds row 8*(r/4) + 4*(lane/32) + r%4,
+    // column lane%32.
+    const int col_in = lane & 31;
+    const int row_in = (lane >> 5) * 4;
+    if constexpr (SWIGLU) {
+        constexpr int HALF_SN = SN / 2;
+#pragma unroll
+        for (int i = 0; i < SM; ++i) {
+#pragma unroll
+            for (int j = 0; j < HALF_SN; ++j) {
+                const int64_t col = static_cast<int64_t>(n_tile) * (BN / 2) + wn * (WTN / 2) + j * 32 + col_in;
+                if (col >= p.n_out) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t grow = row0 + wm * WTM + i * 32 + (r >> 2) * 8 + row_in + (r & 3);
+                    if (grow < row_end) {
+                        const float g = bf16_to_f32(f32_to_bf16(acc[i][j][r]));
+                        const float u = bf16_to_f32(f32_to_bf16(acc[i][j + HALF_SN][r]));
+                        p.c[grow * p.ldc + col] = f32_to_bf16(silu(g) * u);
+                    }
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < SM; ++i) {
+#pragma unroll
+            for (int j = 0; j < SN; ++j) {
+                const int64_t col = static_cast<int64_t>(n_tile) * BN + wn * WTN + j * 32 + col_in;
+                if (col >= p.n_out) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t grow = row0 + wm * WTM + i * 32 + (r >> 2) * 8 + row_in + (r & 3);
+                    if (grow < row_end) p.c[grow * p.ldc + col] = f32_to_bf16(acc[i][j][r]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
+static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
+    const int64_t out_per_tile = SWIGLU ? BN / 2 : BN;
+    p.n_tiles = static_cast<int>((p.n_out + out_per_tile - 1) / out_per_tile);
+    // Upper bound on row tiles: sum_e ceil(span_e/BM) <= ceil(R/BM) + E.
+    const int64_t m_bound = (rows + BM - 1) / BM + p.experts;
+    int64_t blocks = m_bound * p.n_tiles;
+    blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
+    if (blocks == 0) return MOE_OK;
+    if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
+    hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, SWIGLU>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads), 0, stream, p);
+    return check_launch("grouped_gemm_kernel");
+}
+
+int launch_grouped_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, const int32_t* offsets,
+                        int64_t rows, int64_t n, int64_t k, int experts, hipStream_t stream) {
+    GemmParams p{};
+    p.a = a;
+    p.b = b;
+    p.c = c;
+    p.offsets = offsets;
+    p.k = k;
+    p.nb = n;
+    p.n_out = n;
+    p.ldc = n;
+    p.experts = experts;
+    return launch_gemm_t<256, 256, 2, 2, false>(p, rows, stream);
+}
+
+int launch_gateup_swiglu(const uint16_t* a, const uint16_t* gate_up, uint16_t* act,
+                         const int32_t* offsets, int64_t rows, int64_t hidden,
+                         int64_t intermediate, int experts, hipStream_t stream) {
+    GemmParams p{};
+    p.a = a;
+    p.b = gate_up;
+    p.c = act;
+    p.offsets = offsets;
+    p.k = hidden;
+    p.nb = 2 * intermediate;
+    p.n_out = intermediate;
+    p.ldc = intermediate;
+    p.experts = experts;
+    return launch_gemm_t<256, 256, 2, 2, true>(p, rows, stream);
+}
+
+}  // namespace moe

@@ -1,0 +1,257 @@
+"""Tensor-level operators over the C ABI, with the reference extension's names.
+
+``get_extension()`` returns an object exposing the five functions of the
+reference's pybind module (``src/moe_dispatch/_extension.py:52-58``,
+``csrc/bindings.cpp:3-13``): ``dispatch_out``, ``dispatch_aligned_out``,
+``combine_out``, ``swiglu_out`` and ``topk_route_out``, plus the fused router
+and grouped GEMM entry points of this build. Each validates its tensors like
+the reference's ``TORCH_CHECK`` calls (raising ``RuntimeError``) and launches
+on the current torch stream without synchronising.
+"""
+
+from __future__ import annotations
+
+import hashlib
+from functools import lru_cache
+from pathlib import Path
+
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    torch.float32: _lib.DTYPE_F32,
+    torch.float16: _lib.DTYPE_F16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+}
+
+
+def _check(condition, message):
+    if not condition:
+        raise RuntimeError(message)
+
+
+def _check_gpu_tensor(tensor, anchor, name):
+    _check(isinstance(tensor, torch.Tensor), f"{name} must be a tensor")
+    _check(tensor.is_cuda, f"{name}: all tensors must be GPU tensors")
+    _check(tensor.is_contiguous(), f"{name}: all tensors must be contiguous")
+    _check(tensor.device == anchor.device, f"{name}: device mismatch")
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(tensor):
+    return tensor.data_ptr() if tensor is not None else None
+
+
+class HipExtension:
+    """Operators of ``libmoe_hip.so`` on torch tensors."""
+
+    def __init__(self):
+        self.lib = _lib.load_library()
+
+    # -- routing -------------------------------------------------------------
+    def topk_route_out(self, logits, bias, ids32, ids64, weights):
+        """Reference ``csrc/dispatch.cu:378-402``; K up to 8 here."""
+        _check(logits.is_cuda and logits.is_contiguous() and logits.dim() == 2
+               and logits.dtype == torch.float32, "expected FP32 GPU logits[T,E]")
+        for name, t in (("bias", bias), ("ids32", ids32), ("ids64", ids64), ("weights", weights)):
+            _check_gpu_tensor(t, logits, name)
+        tokens, experts = logits.shape
+        _check(1 <= experts <= 64, "routing supports 1..64 experts and int32 indexing")
+        _check(bias.dim() == 1 and bias.numel() == experts and bias.dtype == torch.float32,
+               "expected FP32 bias[E]")
+        _check(ids32.dim() == 2 and ids32.shape[0] == tokens and ids32.dtype == torch.int32,
+               "expected int32 ids[T,K]")
+        topk = ids32.shape[1]
+        _check(1 <= topk <= min(experts, 8) and ids64.shape == ids32.shape
+               and ids64.dtype == torch.int64 and weights.shape == ids32.shape
+               and weights.dtype == torch.float32,
+               "expected top-k (K <= min(E, 8)) int64 IDs and FP32 weights")
+        status = self.lib.moe_topk_route(
+            _ptr(logits), _ptr(bias), _ptr(ids32), _ptr(ids64), _ptr(weights),
+            tokens, experts, topk, _stream(logits.device))
+        self.lib.check(status, "topk_route_out")
+
+    def router_fused_out(self, x, router_weight, bias, ids32, ids64, weights, logits=None):
+        """Fused fp32 router projection + top-k (replaces ``layer.py:123,134``)."""
+        _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,
+               "expected BF16 GPU x[T,H]")
+        tokens, hidden = x.shape
+        for name, t in (("router_weight", router_weight), ("bias", bias), ("ids32", ids32),
+                        ("weights", weights)):
+            _check_gpu_tensor(t, x, name)
+        if ids64 is not None:
+            _check_gpu_tensor(ids64, x, "ids64")
+        experts = router_weight.shape[0]
+        _check(router_weight.dtype == torch.float32 and router_weight.shape == (experts, hidden),
+               "expected FP32 router_weight[E,H]")
+        _check(bias.dtype == torch.float32 and bias.shape == (experts,), "expected FP32 bias[E]")
+        topk = ids32.shape[1] if ids32.dim() == 2 else -1
+        _check(ids32.shape == (tokens, topk) and ids32.dtype == torch.int32, "expected int32 ids[T,K]")
+        _check(weights.shape == (tokens, topk) and weights.dtype == torch.float32,
+               "expected FP32 weights[T,K]")
+        if ids64 is not None:
+            _check(ids64.shape == (tokens, topk) and ids64.dtype == torch.int64, "expected int64 ids[T,K]")
+        if logits is not None:
+            _check_gpu_tensor(logits, x, "logits")
+            _check(logits.shape == (tokens, experts) and logits.dtype == torch.float32,
+                   "expected FP32 logits[T,E]")
+        status = self.lib.moe_router_fused(
+            _ptr(x), _ptr(router_weight), _ptr(bias), _ptr(ids32), _ptr(ids64), _ptr(weights),
+            _ptr(logits), tokens, hidden, experts, topk, _stream(x.device))
+        self.lib.check(status, "router_fused_out")
+
+    # -- transport -----------------------------------------------------------
+    def scratch_bytes(self, tokens, experts, topk):
+        return int(self.lib.moe_dispatch_scratch_bytes(tokens, experts, topk))
+
+    def _dispatch(self, x, ids, counts, offsets, slots, packed, inverse, vectorized, alignment,
+                  scratch, name):
+        _check(x.is_cuda and x.is_contiguous(), "x must be contiguous GPU")
+        _check(x.dim() == 2 and ids.dim() == 2, "expected x[T,H], ids[T,K]")
+        _check(x.dtype in _DTYPES, "only FP32, FP16, and BF16 are supported")
+        _check(ids.dtype == torch.int32, "ids must be int32")
+        tokens, hidden = x.shape
+        topk = ids.shape[1]
+        experts = counts.numel()
+        _check(ids.shape[0] == tokens and hidden > 0, "incompatible token dimensions")
+        _check(1 <= topk <= 8, "topk must be in 1..8")
+        _check(1 <= experts <= 64, "supports 1..64 experts")
+        for t_name, t in (("ids", ids), ("counts", counts), ("offsets", offsets), ("slots", slots),
+                          ("packed", packed), ("inverse", inverse)):
+            _check_gpu_tensor(t, x, t_name)
+        _check(all(t.dtype == torch.int32 for t in (counts, offsets, slots, inverse)),
+               "workspace indices must be int32")
+        n = tokens * topk
+        _check(offsets.numel() == experts + 1 and slots.numel() == n and inverse.numel() == n,
+               "incorrect index workspace size")
+        _check(packed.dim() == 2 and packed.shape[1] == hidden and packed.dtype == x.dtype,
+               "incorrect packed workspace")
+        need = self.scratch_bytes(tokens, experts, topk)
+        if scratch is None:
+            scratch = torch.empty(max(need, 4), dtype=torch.uint8, device=x.device)
+        _check_gpu_tensor(scratch, x, "scratch")
+        status = self.lib.moe_dispatch(
+            _ptr(x), _DTYPES[x.dtype], _ptr(ids), _ptr(counts), _ptr(offsets), _ptr(slots),
+            _ptr(packed), _ptr(inverse), _ptr(scratch), scratch.numel() * scratch.element_size(),
+            tokens, hidden, experts, topk, alignment, packed.shape[0], int(bool(vectorized)),
+            _stream(x.device))
+        self.lib.check(status, name)
+
+    def dispatch_out(self, x, ids, counts, offsets, slots, packed, inverse, vectorized,
+                     scratch=None):
+        """Compact dispatch (reference ``csrc/dispatch.cu:102-158``)."""
+        self._dispatch(x, ids, counts, offsets, slots, packed, inverse, vectorized, 1, scratch,
+                       "dispatch_out")
+
+    def dispatch_aligned_out(self, x, ids, counts, offsets, slots, packed, inverse, vectorized,
+                             alignment, scratch=None):
+        """Aligned dispatch with zeroed padding (reference ``csrc/dispatch.cu:218-275``)."""
+        _check(1 <= alignment <= 128, "alignment must be 1..128")
+        self._dispatch(x, ids, counts, offsets, slots, packed, inverse, vectorized, alignment,
+                       scratch, "dispatch_aligned_out")
+
+    def combine_out(self, packed_output, inverse, weights, output):
+        """Weighted gather-reduce (reference ``csrc/dispatch.cu:160-192``)."""
+        _check(packed_output.is_cuda and packed_output.is_contiguous(),
+               "expert output must be contiguous GPU")
+        _check(output.dim() == 2 and inverse.dim() == 2 and weights.dim() == 2,
+               "expected output[T,H], inverse[T,K], weights[T,K]")
+        _check(packed_output.dim() == 2 and packed_output.dtype in _DTYPES, "unsupported output dtype")
+        for name, t in (("inverse", inverse), ("weights", weights), ("output", output)):
+            _check_gpu_tensor(t, packed_output, name)
+        _check(inverse.dtype == torch.int32 and weights.dtype == torch.float32,
+               "inverse must be int32; weights must be FP32")
+        tokens, hidden = output.shape
+        topk = inverse.shape[1]
+        _check(1 <= topk <= 8, "topk must be in 1..8")
+        _check(hidden > 0, "invalid output shape")
+        _check(inverse.shape[0] == tokens and weights.shape == inverse.shape
+               and packed_output.shape[0] >= tokens * topk and packed_output.shape[1] == hidden
+               and output.dtype == packed_output.dtype, "shape/dtype mismatch")
+        status = self.lib.moe_combine(
+            _ptr(packed_output), _DTYPES[packed_output.dtype], _ptr(inverse), _ptr(weights),
+            _ptr(output), tokens, hidden, topk, packed_output.shape[0],
+            _stream(packed_output.device))
+        self.lib.check(status, "combine_out")
+
+    # -- expert compute ------------------------------------------------------
+    def swiglu_out(self, projection, valid_rows, output):
+        """Standalone SwiGLU (reference ``csrc/dispatch.cu:294-323``)."""
+        _check(projection.is_cuda and projection.is_contiguous(), "projection must be contiguous GPU")
+        _check(projection.dim() == 2 and output.dim() == 2
+               and projection.shape[0] == output.shape[0]
+               and projection.shape[1] == output.shape[1] * 2,
+               "expected projection[R,2I], output[R,I]")
+        _check_gpu_tensor(valid_rows, projection, "valid_rows")
+        _check_gpu_tensor(output, projection, "output")
+        _check(valid_rows.dtype == torch.int32 and valid_rows.numel() == 1,
+               "valid_rows must be a single int32 GPU value")
+        _check(output.dtype == projection.dtype and projection.dtype in _DTYPES, "unsupported dtype")
+        status = self.lib.moe_swiglu(
+            _ptr(projection), _DTYPES[projection.dtype], _ptr(valid_rows), _ptr(output),
+            output.shape[0], output.shape[1], _stream(projection.device))
+        self.lib.check(status, "swiglu_out")
+
+    def grouped_gemm_out(self, x, weight, offsets, output):
+        """``output[r] = x[r] @ weight[e]^T`` for rows of expert e (bf16, fp32 accumulate)."""
+        self._check_gemm(x, weight, offsets, output, weight.shape[1])
+        status = self.lib.moe_grouped_gemm(
+            _ptr(x), _ptr(weight), _ptr(output), _ptr(offsets), x.shape[0], weight.shape[1],
+            x.shape[1], weight.shape[0], _stream(x.device))
+        self.lib.check(status, "grouped_gemm_out")
+
+    def gateup_swiglu_out(self, x, gate_up, offsets, output):
+        """Gate/up grouped GEMM with the SwiGLU epilogue fused; output is ``[R, I]``."""
+        _check(gate_up.dim() == 3 and gate_up.shape[1] % 2 == 0, "expected gate_up[E,2I,H]")
+        self._check_gemm(x, gate_up, offsets, output, gate_up.shape[1] // 2)
+        status = self.lib.moe_grouped_gateup_swiglu(
+            _ptr(x), _ptr(gate_up), _ptr(output), _ptr(offsets), x.shape[0], x.shape[1],
+            gate_up.shape[1] // 2, gate_up.shape[0], _stream(x.device))
+        self.lib.check(status, "gateup_swiglu_out")
+
+    @staticmethod
+    def _check_gemm(x, weight, offsets, output, out_cols):
+        _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,
+               "expected contiguous BF16 GPU x[R,K]")
+        for name, t in (("weight", weight), ("offsets", offsets), ("output", output)):
+            _check_gpu_tensor(t, x, name)
+        _check(weight.dim() == 3 and weight.dtype == torch.bfloat16 and weight.shape[2] == x.shape[1],
+               "expected BF16 weight[E,N,K] matching x")
+        _check(offsets.dtype == torch.int32 and offsets.numel() == weight.shape[0] + 1,
+               "expected int32 offsets[E+1]")
+        _check(output.shape == (x.shape[0], out_cols) and output.dtype == torch.bfloat16,
+               "incorrect grouped-GEMM output buffer")
+        _check(x.shape[1] % 8 == 0 and out_cols % 8 == 0, "grouped GEMM dimensions must be multiples of 8")
+
+
+@lru_cache(maxsize=1)
+def get_extension():
+    """The HIP operator set (reference ``_extension.py:30-63``), loaded once.
+
+    Raises ``RuntimeError`` without a GPU or when ``libmoe_hip.so`` is missing:
+    there is no eager or CPU fallback.
+    """
+    if not torch.cuda.is_available():
+        raise RuntimeError("HIP operators require an AMD GPU (MI355X / gfx950). Use the torch "
+                           "implementation on CPU.")
+    return HipExtension()
+
+
+def source_texts():
+    """Kernel and ABI sources, for provenance hashes."""
+    root = Path(__file__).resolve().parents[1] / "csrc"
+    header = Path(__file__).resolve().parents[2] / "include" / "moe_hip.h"
+    files = sorted(root.glob("*.hip")) + sorted(root.glob("*.h")) + [header]
+    return {f.name: f.read_text() for f in files if f.is_file()}
+
+
+def source_hashes():
+    """sha256 of every kernel source and package module (reference ``_extension.py:18-27``)."""
+    result = {name: hashlib.sha256(text.encode()).hexdigest() for name, text in source_texts().items()}
+    for source in Path(__file__).resolve().parent.glob("*.py"):
+        result[source.name] = hashlib.sha256(source.read_bytes()).hexdigest()
+    return result

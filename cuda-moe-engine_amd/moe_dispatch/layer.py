@@ -1,0 +1,236 @@
+"""A complete single-GPU MoE feed-forward block with matched implementation variants.
+
+Mirrors ``src/moe_dispatch/layer.py:12-214``: ``MoEConfig``, ``MoEWeights``,
+``make_weights``, ``LayerWorkspace``, ``MoEBlock`` (``route``, ``workspace``,
+``experts_forward``, ``forward``, ``set_routing_pattern``) and
+``token_major_oracle``. Implementations:
+
+* ``cuda_fused``: HIP fused router (fp32 logits + bias + top-k + softmax),
+  HIP dispatch, HIP gate/up GEMM with the SwiGLU epilogue, HIP down GEMM, HIP
+  combine. The drop-in for the reference's ``cuda_fused``.
+* ``cuda``: PyTorch router, HIP transport, HIP GEMMs with a separate
+  PyTorch SwiGLU.
+* ``torch``: the PyTorch variant (CPU or GPU), used as the baseline.
+
+Top-k may be 1..8 (the reference allows 1 or 2); ``set_routing_bias`` sets an
+arbitrary router bias.
+"""
+
+from dataclasses import dataclass
+import math
+
+import torch
+
+from ._extension import get_extension
+from .experts import grouped_linear, resolve_backend, swiglu_reference
+from .reference import TorchWorkspace
+from .workspace import MAX_EXPERTS, MAX_TOPK, CudaWorkspace
+
+IMPLEMENTATIONS = ("torch", "cuda", "cuda_fused")
+
+
+@dataclass(frozen=True)
+class MoEConfig:
+    hidden: int = 512
+    intermediate: int = 1024
+    experts: int = 8
+    topk: int = 2
+    alignment: int = 8
+
+    def __post_init__(self):
+        if self.hidden < 8 or self.intermediate < 8:
+            raise ValueError("hidden/intermediate must be at least 8")
+        if self.hidden % 8 or self.intermediate % 8:
+            raise ValueError("grouped GEMM dimensions must be multiples of 8")
+        if (
+            not 1 <= self.experts <= MAX_EXPERTS
+            or not 1 <= self.topk <= MAX_TOPK
+            or self.topk > self.experts
+        ):
+            raise ValueError("invalid expert/topk configuration")
+        if not 8 <= self.alignment <= 128 or self.alignment % 8:
+            raise ValueError("full-block grouped GEMM alignment must be a multiple of 8 up to 128")
+
+
+@dataclass
+class MoEWeights:
+    router: torch.Tensor
+    gate_up: torch.Tensor
+    down: torch.Tensor
+
+
+def make_weights(config, device, dtype, seed=42):
+    """Seeded weights, drawn in the reference's order (``layer.py:38-59``).
+
+    router ``[E,H]`` fp32 ~ N(0,1/H); gate_up ``[E,2I,H]`` ~ N(0,1/H) and down
+    ``[E,H,I]`` ~ N(0,1/I), both cast to ``dtype``.
+    """
+    generator = torch.Generator(device=device).manual_seed(seed)
+    e, h, i = config.experts, config.hidden, config.intermediate
+    router = torch.randn(e, h, device=device, generator=generator) / math.sqrt(h)
+    gate_up = (torch.randn(e, 2 * i, h, device=device, generator=generator) / math.sqrt(h)).to(dtype)
+    down = (torch.randn(e, h, i, device=device, generator=generator) / math.sqrt(i)).to(dtype)
+    return MoEWeights(router, gate_up, down)
+
+
+@dataclass
+class LayerWorkspace:
+    transport: object
+    projection: torch.Tensor
+    activated: torch.Tensor
+    expert_output: torch.Tensor
+
+
+class MoEBlock(torch.nn.Module):
+    """Inference-only top-k MoE: router, dispatch, two grouped GEMMs, SwiGLU, combine.
+
+    Output is a reusable view: clone it before the next call.
+    """
+
+    def __init__(
+        self,
+        config=None,
+        *,
+        device="cuda",
+        dtype=torch.bfloat16,
+        implementation="cuda_fused",
+        expert_backend="auto",
+        seed=42,
+        weights=None,
+    ):
+        super().__init__()
+        self.config = config or MoEConfig()
+        if implementation not in IMPLEMENTATIONS:
+            raise ValueError("implementation must be torch, cuda, or cuda_fused")
+        device = torch.device(device)
+        if implementation != "torch" and device.type != "cuda":
+            raise RuntimeError("HIP implementations require a GPU")
+        if device.type == "cuda" and dtype != torch.bfloat16:
+            raise ValueError("full GPU block uses BF16 grouped GEMMs")
+        self.implementation = implementation
+        backend = resolve_backend(device, expert_backend)
+        if implementation != "torch" and backend != "hip":
+            raise ValueError("HIP implementations use the HIP grouped GEMM (expert_backend='hip')")
+        self.expert_backend = backend
+        weights = weights or make_weights(self.config, device, dtype, seed)
+        cfg = self.config
+        if weights.gate_up.shape != (cfg.experts, 2 * cfg.intermediate, cfg.hidden) or (
+            weights.down.shape != (cfg.experts, cfg.hidden, cfg.intermediate)
+        ):
+            raise ValueError("expert weights do not match the block configuration")
+        if weights.router.shape != (cfg.experts, cfg.hidden):
+            raise ValueError("router weights do not match the block configuration")
+        self.register_buffer("router_weight", weights.router.contiguous())
+        self.register_buffer("gate_up_weight", weights.gate_up.contiguous())
+        self.register_buffer("down_weight", weights.down.contiguous())
+        self.register_buffer("routing_bias", torch.zeros(cfg.experts, device=device))
+        self._workspaces = {}
+        self._route_buffers = {}
+        self._extension = get_extension() if implementation != "torch" else None
+
+    def set_routing_pattern(self, pattern):
+        if pattern not in ("balanced", "skewed"):
+            raise ValueError("routing pattern must be balanced or skewed")
+        self.routing_bias.zero_()
+        if pattern == "skewed":
+            self.routing_bias[: self.config.topk] = 5.0
+
+    def set_routing_bias(self, bias):
+        """Set an arbitrary fp32 router bias ``[E]`` (e.g. a Zipf-shaped skew)."""
+        bias = torch.as_tensor(bias, dtype=torch.float32)
+        if bias.shape != (self.config.experts,):
+            raise ValueError("routing bias must have shape [experts]")
+        self.routing_bias.copy_(bias)
+
+    def route(self, x):
+        if self.implementation == "cuda_fused":
+            key = (x.shape[0], x.device)
+            if key not in self._route_buffers:
+                shape = (x.shape[0], self.config.topk)
+                self._route_buffers[key] = (
+                    torch.empty(shape, device=x.device, dtype=torch.int32),
+                    torch.empty(shape, device=x.device, dtype=torch.int64),
+                    torch.empty(shape, device=x.device, dtype=torch.float32),
+                )
+            ids32, ids64, weights = self._route_buffers[key]
+            self._extension.router_fused_out(
+                x, self.router_weight, self.routing_bias, ids32, ids64, weights
+            )
+            return ids32, ids64, weights
+        logits = torch.nn.functional.linear(x.float(), self.router_weight) + self.routing_bias
+        selected, ids64 = torch.topk(logits, self.config.topk, dim=-1)
+        weights = torch.softmax(selected, dim=-1).contiguous()
+        return ids64.to(torch.int32).contiguous(), ids64.contiguous(), weights
+
+    def workspace(self, x):
+        key = (x.shape[0], x.dtype, x.device)
+        if key not in self._workspaces:
+            cfg = self.config
+            common = (x.shape[0], cfg.hidden, cfg.experts, cfg.topk, x.dtype)
+            if self.implementation == "torch":
+                transport = TorchWorkspace(*common, device=x.device, alignment=cfg.alignment)
+            else:
+                transport = CudaWorkspace(
+                    *common, device=x.device, alignment=cfg.alignment, extension=self._extension
+                )
+            rows = transport.capacity_rows
+            # The fused gate/up kernel never materialises the [R, 2I] projection.
+            proj_rows = 0 if self.implementation == "cuda_fused" else rows
+            self._workspaces[key] = LayerWorkspace(
+                transport,
+                torch.empty((proj_rows, 2 * cfg.intermediate), device=x.device, dtype=x.dtype),
+                torch.empty((rows, cfg.intermediate), device=x.device, dtype=x.dtype),
+                torch.empty((rows, cfg.hidden), device=x.device, dtype=x.dtype),
+            )
+        return self._workspaces[key]
+
+    def experts_forward(self, state):
+        transport = state.transport
+        offsets = transport.offsets
+        if self.implementation == "cuda_fused":
+            ext = self._extension
+            ext.gateup_swiglu_out(transport.packed, self.gate_up_weight, offsets, state.activated)
+            ext.grouped_gemm_out(state.activated, self.down_weight, offsets, state.expert_output)
+            return state.expert_output
+        ends = offsets[1:]
+        grouped_linear(
+            transport.packed, self.gate_up_weight, ends, backend=self.expert_backend,
+            output=state.projection, offsets=offsets,
+        )
+        state.activated.copy_(swiglu_reference(state.projection))
+        grouped_linear(
+            state.activated, self.down_weight, ends, backend=self.expert_backend,
+            output=state.expert_output, offsets=offsets,
+        )
+        return state.expert_output
+
+    @torch.inference_mode()
+    def forward(self, x):
+        if x.ndim != 2 or x.shape[1] != self.config.hidden or not x.is_contiguous():
+            raise ValueError("expected contiguous x[T,hidden]")
+        if x.dtype != self.gate_up_weight.dtype or x.device != self.gate_up_weight.device:
+            raise ValueError("input dtype/device must match expert weights")
+        if x.shape[0] == 0:
+            return torch.empty_like(x)
+        state = self.workspace(x)
+        ids32, ids64, weights = self.route(x)
+        state.transport.dispatch(x, ids32, ids64)
+        output = self.experts_forward(state)
+        state.transport.combine(output, weights)
+        return state.transport.output
+
+
+@torch.inference_mode()
+def token_major_oracle(block, x):
+    """Dense token-major expert evaluation (reference ``layer.py:200-214``); excluded from timings."""
+    logits = torch.nn.functional.linear(x.float(), block.router_weight) + block.routing_bias
+    selected, ids64 = torch.topk(logits, block.config.topk, dim=-1)
+    weights = torch.softmax(selected, dim=-1)
+    expected = torch.zeros_like(x, dtype=torch.float32)
+    for expert in range(block.config.experts):
+        projection = torch.nn.functional.linear(x, block.gate_up_weight[expert])
+        activation = swiglu_reference(projection)
+        output = torch.nn.functional.linear(activation, block.down_weight[expert])
+        probability = (weights * (ids64 == expert)).sum(dim=1)
+        expected += output.float() * probability[:, None]
+    return expected.to(x.dtype)

@@ -1,0 +1,35 @@
+"""Seeded synthetic routed-token inputs, generated outside timed regions.
+
+Restates ``make_case`` (reference ``src/moe_dispatch/routing.py:6-17``): from
+one seeded generator, x ~ N(0,1) in the requested dtype, then fp32 logits
+~ N(0,1) (``skewed`` adds 5 to the first K experts), top-k, softmax of the
+selected logits.
+"""
+
+import torch
+
+
+def make_case(tokens, hidden, experts, topk, dtype, pattern, seed, device="cuda"):
+    generator = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn((tokens, hidden), device=device, dtype=dtype, generator=generator)
+    logits = torch.randn((tokens, experts), device=device, generator=generator)
+    if pattern == "skewed":
+        logits[:, :topk] += 5.0
+    elif pattern != "balanced":
+        raise ValueError(f"unknown pattern: {pattern}")
+    selected, ids64 = torch.topk(logits, topk, dim=-1)
+    weights = torch.softmax(selected, dim=-1).contiguous()
+    return x, ids64.to(torch.int32).contiguous(), ids64.contiguous(), weights
+
+
+def make_transport_case(tokens, hidden, experts, topk, dtype, seed, device="cuda"):
+    """Transport workload with i.i.d. uniform expert ids (duplicates within a token allowed).
+
+    x ~ N(0,1); ids ~ randint(0, E); weights = softmax of N(0,1) logits [T,K].
+    """
+    generator = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn((tokens, hidden), device=device, dtype=dtype, generator=generator)
+    ids64 = torch.randint(0, experts, (tokens, topk), device=device, generator=generator)
+    logits = torch.randn((tokens, topk), device=device, generator=generator)
+    weights = torch.softmax(logits, dim=-1).contiguous()
+    return x, ids64.to(torch.int32).contiguous(), ids64.contiguous(), weights

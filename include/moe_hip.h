@@ -1,0 +1,159 @@
+/*
+ * moe_hip.h - C ABI of the gfx950 (MI355X) MoE feed-forward kernels.
+ *
+ * Every entry point takes raw device pointers, 64-bit sizes and a HIP stream
+ * (hipStream_t passed as void*; NULL means the default stream). Calls are
+ * asynchronous on that stream, never synchronise the host, and never allocate
+ * or free device memory: the caller owns every buffer, including the scratch
+ * that moe_dispatch needs (size from moe_dispatch_scratch_bytes).
+ *
+ * Return value: MOE_OK (0) or a moe_status_t error code. moe_last_error()
+ * returns a thread-local message describing the most recent failure.
+ *
+ * Layouts (all row-major, contiguous):
+ *   x            [T, H]       activations (bf16 for the block; f32/f16/bf16 transport)
+ *   router_w     [E, H]       fp32
+ *   ids32/ids64  [T, K]       selected experts, flat assignment index p = t*K + k
+ *   weights      [T, K]       fp32 routing weights
+ *   counts       [E]          int32 assignments per expert
+ *   offsets      [E+1]        int32 start row of each expert's span in `packed`
+ *   slots        [T*K]        int32 within-expert slot of each assignment
+ *   inverse      [T, K]       int32 packed row of each assignment
+ *   packed       [R, H]       rows grouped by expert; span e = [offsets[e], offsets[e+1])
+ *   gate_up      [E, 2I, H]   bf16; rows 0..I-1 gate, I..2I-1 up
+ *   down         [E, H, I]    bf16
+ *
+ * Slot order is canonical (deterministic): within an expert, assignments
+ * appear in increasing flat index p. No global atomics are used.
+ */
+#ifndef MOE_HIP_H_
+#define MOE_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_ABI_VERSION 1
+
+typedef enum {
+    MOE_DTYPE_F32 = 0,
+    MOE_DTYPE_F16 = 1,
+    MOE_DTYPE_BF16 = 2,
+} moe_dtype_t;
+
+typedef enum {
+    MOE_OK = 0,
+    MOE_ERR_INVALID_ARGUMENT = 1, /* shape, pointer or dtype mismatch */
+    MOE_ERR_UNSUPPORTED = 2,      /* valid request outside this build's limits */
+    MOE_ERR_CAPACITY = 3,         /* exceeds int32 indexing capacity */
+    MOE_ERR_WORKSPACE = 4,        /* caller buffer too small */
+    MOE_ERR_HIP = 5,              /* HIP runtime / launch failure */
+} moe_status_t;
+
+/* ABI version of the loaded library (MOE_ABI_VERSION at build time). */
+int moe_abi_version(void);
+
+/* Static description of a status code. */
+const char* moe_status_string(int status);
+
+/* Thread-local message for the most recent non-OK return on this thread. */
+const char* moe_last_error(void);
+
+/*
+ * Top-k routing on given fp32 logits.
+ * Replaces topk_route_out (reference src/moe_dispatch/csrc/dispatch.cu:378-402,
+ * kernel :338-376, tie rule :325-336; binding csrc/bindings.cpp:12-13).
+ * v = logits + bias; top-k by value with ties to the lower expert index;
+ * weights: K=1 -> 1, K=2 -> w0 = 1/(1+exp(v1-v0)), w1 = exp(v1-v0)*w0,
+ * K>2 -> exp(v_j - v_0) / sum_i exp(v_i - v_0).
+ * Limits: 1 <= E <= 64, 1 <= K <= min(E, 8), T*E <= INT32_MAX. Logits must be finite.
+ */
+int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64_t* ids64,
+                   float* weights, int64_t tokens, int64_t experts, int64_t topk, void* stream);
+
+/*
+ * Fused router: logits = float(x) . router_w^T in fp32, then moe_topk_route's
+ * selection. Replaces the F.linear + topk_route_out pair of MoEBlock.route
+ * (reference src/moe_dispatch/layer.py:122-135). x is bf16 [T,H]. logits_out
+ * ([T,E] fp32) is optional (NULL to skip). ids64 may be NULL.
+ */
+int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
+                     int64_t* ids64, float* weights, float* logits_out, int64_t tokens,
+                     int64_t hidden, int64_t experts, int64_t topk, void* stream);
+
+/* Bytes of scratch moe_dispatch needs for (T, E, K). */
+int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk);
+
+/*
+ * Token dispatch: expert histogram, prefix scan and stable pack.
+ * Replaces dispatch_out (alignment == 1; reference csrc/dispatch.cu:102-158)
+ * and dispatch_aligned_out (alignment > 1; :218-275), binding
+ * csrc/bindings.cpp:2-4,7-9.
+ *   counts[e]  = #{p : ids[p] == e}
+ *   offsets[0] = 0, offsets[e+1] = offsets[e] + ceil(counts[e]/a)*a
+ *   slots[p]   = #{p' < p : ids[p'] == ids[p]}     (canonical order)
+ *   inverse[p] = offsets[ids[p]] + slots[p]
+ *   packed[inverse[p]] = x[p / K]; rows [offsets[e]+counts[e], offsets[e+1]) = 0.
+ * Rows >= offsets[E] are not written. Out-of-range ids are skipped (slot -1,
+ * inverse untouched) as in the reference kernels.
+ * vectorized != 0 copies rows with 16-byte accesses when the row size allows.
+ * packed_rows must be >= T*K (alignment 1) or the aligned capacity
+ * ceil((T*K + E*(a-1) + 1)/a)*a (reference src/moe_dispatch/workspace.py:29-34).
+ * Limits: 1 <= E <= 64, 1 <= K <= 8, 1 <= a <= 128, H >= 1.
+ */
+int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                 int32_t* slots, void* packed, int32_t* inverse, void* scratch,
+                 int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                 int64_t topk, int64_t alignment, int64_t packed_rows, int vectorized,
+                 void* stream);
+
+/*
+ * Weighted combine: out[t] = round(sum_k w[t,k] * float(y[inverse[t,k]])),
+ * fp32 products and running sum in k order (no fused multiply-add), rows
+ * outside [0, packed_rows) skipped, no atomics.
+ * Replaces combine_out (reference csrc/dispatch.cu:160-192, kernel :76-93;
+ * binding csrc/bindings.cpp:5-6).
+ */
+int moe_combine(const void* expert_output, int dtype, const int32_t* inverse,
+                const float* weights, void* output, int64_t tokens, int64_t hidden,
+                int64_t topk, int64_t packed_rows, void* stream);
+
+/*
+ * SwiGLU: out[r, j] = round(silu(g) * u), g = proj[r, j], u = proj[r, I + j],
+ * fp32 math, one cast; rows >= *valid_rows (device int32) are exactly zero.
+ * Replaces swiglu_out (reference csrc/dispatch.cu:294-323, kernel :277-292;
+ * binding csrc/bindings.cpp:10).
+ */
+int moe_swiglu(const void* projection, int dtype, const int32_t* valid_rows, void* output,
+               int64_t rows, int64_t width, void* stream);
+
+/*
+ * Grouped bf16 GEMM on MFMA: for every expert e and row r in
+ * [offsets[e], offsets[e+1]):  c[r, :] = round_bf16(a[r, :] . b[e]^T)
+ * with fp32 accumulation. a [rows, k], b [E, n, k], c [rows, n].
+ * Rows at or past offsets[E] are not written.
+ * Replaces grouped_linear -> grouped_mm (reference src/moe_dispatch/experts.py:21-35,
+ * _triton_gemm.py:16-104; ENDS = offsets[1:]). Requires n % 8 == 0, k % 8 == 0.
+ */
+int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offsets,
+                     int64_t rows, int64_t n, int64_t k, int64_t experts, void* stream);
+
+/*
+ * Grouped gate/up GEMM with the SwiGLU epilogue fused:
+ *   g = round_bf16(a[r] . gate_up[e, j]), u = round_bf16(a[r] . gate_up[e, I + j])
+ *   act[r, j] = round_bf16(silu(g) * u)
+ * which equals grouped_gemm followed by swiglu (reference layer.py:161-172,
+ * csrc/dispatch.cu:277-292) value for value. Rows at or past offsets[E] are
+ * not written. Requires hidden % 8 == 0, intermediate % 8 == 0.
+ */
+int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
+                              const int32_t* offsets, int64_t rows, int64_t hidden,
+                              int64_t intermediate, int64_t experts, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_HIP_H_ */

@@ -1,0 +1,89 @@
+"""Grouped GEMM parity: the MFMA kernels against a float64 per-expert matmul.
+
+Covers empty experts, skewed row counts, partial row tiles (spans that are not
+multiples of the row tile), short reductions (K < 64), column counts that are
+not multiples of the column tile, and the fused gate/up + SwiGLU epilogue,
+whose result must equal grouped GEMM -> bf16 projection -> SwiGLU.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as oracle
+from tests._helpers import gpu, rel_l2, to_np
+
+pytestmark = gpu
+
+
+def _offsets(counts, alignment):
+    spans = [(c + alignment - 1) // alignment * alignment for c in counts]
+    return np.concatenate([[0], np.cumsum(spans)]).astype(np.int32)
+
+
+def _inputs(counts, alignment, k, seed):
+    offsets = _offsets(counts, alignment)
+    rows = int(offsets[-1]) + 5  # spare rows past offsets[E] must stay untouched
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    a = torch.randn(rows, k, device="cuda", generator=g).bfloat16()
+    return a, torch.tensor(offsets, device="cuda"), rows
+
+
+GEMM_CASES = [
+    # counts per expert, alignment, n, k
+    ([5, 0, 37, 300, 8, 0, 1, 64], 8, 256, 64),
+    ([0, 0, 0, 1], 8, 512, 128),
+    ([700, 3, 0, 260], 8, 384, 32),
+    ([1024, 1030, 998, 1051], 8, 264, 200),
+    ([33] * 16, 1, 128, 1024),
+    ([2000, 0], 8, 1024, 512),
+]
+
+
+@pytest.mark.parametrize("counts,alignment,n,k", GEMM_CASES)
+def test_grouped_gemm_matches_float64(ext, counts, alignment, n, k):
+    experts = len(counts)
+    a, offsets, rows = _inputs(counts, alignment, k, seed=n + k)
+    b = (torch.randn(experts, n, k, device="cuda") / k**0.5).bfloat16()
+    c = torch.full((rows, n), 7.0, device="cuda").bfloat16()
+    ext.grouped_gemm_out(a, b, offsets, c)
+    exact = oracle.grouped_gemm(to_np(a), to_np(b), to_np(offsets))
+    used = int(to_np(offsets)[-1])
+    got = to_np(c)
+    ref = exact[:used]
+    # bf16 output: at most one rounding of the fp32 accumulator away from the exact value.
+    assert np.all(np.abs(got[:used] - ref) <= 2.0**-8 * np.abs(ref) + 1e-4), "beyond one bf16 rounding"
+    assert rel_l2(got[:used], oracle.bf16_round(ref)) < 2e-3
+    assert np.all(got[used:] == 7.0), "rows past offsets[E] must not be written"
+
+
+GATEUP_CASES = [
+    # counts, alignment, hidden, intermediate
+    ([5, 0, 37, 300, 8, 0, 1, 64], 8, 64, 128),
+    ([0, 1], 8, 256, 256),
+    ([700, 3, 0, 260], 8, 32, 384),
+    ([129, 255, 256, 257], 8, 512, 136),
+    ([2000, 17], 8, 1024, 1408),
+]
+
+
+@pytest.mark.parametrize("counts,alignment,hidden,inter", GATEUP_CASES)
+def test_gateup_swiglu_matches_unfused_pipeline(ext, counts, alignment, hidden, inter):
+    experts = len(counts)
+    a, offsets, rows = _inputs(counts, alignment, hidden, seed=hidden + inter)
+    w = (torch.randn(experts, 2 * inter, hidden, device="cuda") / hidden**0.5).bfloat16()
+    act = torch.full((rows, inter), 3.0, device="cuda").bfloat16()
+    ext.gateup_swiglu_out(a, w, offsets, act)
+    used = int(to_np(offsets)[-1])
+    proj = oracle.bf16_round(oracle.grouped_gemm(to_np(a), to_np(w), to_np(offsets)))
+    ref = oracle.swiglu(proj, used)[:used]
+    got = to_np(act)
+    assert rel_l2(got[:used], ref) < 3e-3
+    np.testing.assert_allclose(got[:used], ref, rtol=2e-2, atol=2e-3)
+    assert np.all(got[used:] == 3.0), "rows past offsets[E] must not be written"
+    # The same kernels unfused (plain GEMM -> standalone SwiGLU) agree within one bf16 step.
+    projection = torch.empty(rows, 2 * inter, device="cuda", dtype=torch.bfloat16)
+    ext.grouped_gemm_out(a, w, offsets, projection)
+    unfused = torch.empty_like(act)
+    ext.swiglu_out(projection, offsets[-1:], unfused)
+    np.testing.assert_allclose(got[:used], to_np(unfused)[:used], rtol=2e-2, atol=2e-3)

@@ -1,0 +1,95 @@
+"""Routing parity: top-k on given logits (bit-exact ids) and the fused fp32 router.
+
+Mirrors the reference's tests/test_gpu_router.py:11-38 (exact ids vs an
+independent top-k, weights within 2e-6, zero-logit tie KAT, empty batch) and
+extends K to 1..8 and E to 1..64.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as oracle
+from tests._helpers import gpu, route_margin, to_np
+
+pytestmark = gpu
+
+
+def _route(ext, logits, bias, topk):
+    tokens = logits.shape[0]
+    ids32 = torch.empty(tokens, topk, device="cuda", dtype=torch.int32)
+    ids64 = torch.empty(tokens, topk, device="cuda", dtype=torch.int64)
+    weights = torch.empty(tokens, topk, device="cuda")
+    ext.topk_route_out(logits, bias, ids32, ids64, weights)
+    return ids32, ids64, weights
+
+
+@pytest.mark.parametrize("experts", [1, 2, 8, 16, 33, 64])
+@pytest.mark.parametrize("topk", [1, 2, 6, 8])
+def test_topk_route_matches_oracle_and_torch(ext, experts, topk):
+    if topk > experts:
+        pytest.skip("topk > experts")
+    generator = torch.Generator(device="cuda").manual_seed(42)
+    logits = torch.randn(257, experts, device="cuda", generator=generator)
+    bias = torch.randn(experts, device="cuda", generator=generator)
+    ids32, ids64, weights = _route(ext, logits, bias, topk)
+    ids_ref, w_ref, _ = oracle.topk_route(to_np(logits), to_np(bias), topk)
+    np.testing.assert_array_equal(to_np(ids32), ids_ref)
+    np.testing.assert_array_equal(to_np(ids64), ids_ref.astype(np.int64))
+    np.testing.assert_allclose(to_np(weights), w_ref, rtol=2e-6, atol=2e-6)
+    # Independent library check (continuous scores: no ties).
+    selected, expected = torch.topk(logits + bias, topk, dim=-1)
+    torch.testing.assert_close(ids64, expected, rtol=0, atol=0)
+    torch.testing.assert_close(weights, selected.softmax(-1), rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("topk", [2, 6])
+def test_topk_route_ties_go_to_lower_expert(ext, topk):
+    generator = torch.Generator(device="cuda").manual_seed(7)
+    logits = torch.randint(0, 3, (513, 64), device="cuda", generator=generator).float()
+    bias = torch.zeros(64, device="cuda")
+    ids32, _, weights = _route(ext, logits, bias, topk)
+    ids_ref, w_ref, _ = oracle.topk_route(to_np(logits), to_np(bias), topk)
+    np.testing.assert_array_equal(to_np(ids32), ids_ref)
+    np.testing.assert_allclose(to_np(weights), w_ref, rtol=2e-6, atol=2e-6)
+
+
+def test_zero_logits_known_answer_and_empty_batch(ext):
+    for tokens in (0, 5):
+        logits = torch.zeros(tokens, 64, device="cuda")
+        bias = torch.zeros(64, device="cuda")
+        _, ids64, weights = _route(ext, logits, bias, 2)
+        expected = torch.tensor([0, 1], device="cuda").expand(tokens, 2)
+        torch.testing.assert_close(ids64, expected, rtol=0, atol=0)
+        torch.testing.assert_close(weights, torch.full_like(weights, 0.5), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize(
+    "tokens,hidden,experts,topk",
+    [(1, 512, 8, 2), (33, 512, 8, 1), (257, 1024, 16, 2), (300, 2048, 64, 6), (64, 4096, 8, 2),
+     (100, 136, 5, 3)],
+)
+def test_fused_router_matches_oracle(ext, tokens, hidden, experts, topk):
+    generator = torch.Generator(device="cuda").manual_seed(tokens + hidden)
+    x = torch.randn(tokens, hidden, device="cuda", generator=generator).bfloat16()
+    w = torch.randn(experts, hidden, device="cuda", generator=generator) / hidden**0.5
+    bias = torch.randn(experts, device="cuda", generator=generator) * 0.1
+    ids32 = torch.empty(tokens, topk, device="cuda", dtype=torch.int32)
+    ids64 = torch.empty(tokens, topk, device="cuda", dtype=torch.int64)
+    weights = torch.empty(tokens, topk, device="cuda")
+    logits = torch.empty(tokens, experts, device="cuda")
+    ext.router_fused_out(x, w, bias, ids32, ids64, weights, logits)
+    ref_logits = oracle.router_logits(to_np(x), to_np(w))
+    got_logits = to_np(logits)
+    # fp32 dot products in a different order: bounded by a few ulp of the row norm.
+    scale = np.linalg.norm(to_np(x), axis=1)[:, None] * np.linalg.norm(to_np(w), axis=1)[None, :]
+    assert np.all(np.abs(got_logits - ref_logits) <= 1e-6 * scale + 1e-7)
+    # Selection on the kernel's own logits is bit-exact against the oracle.
+    ids_on_got, w_on_got, _ = oracle.topk_route(got_logits, to_np(bias), topk)
+    np.testing.assert_array_equal(to_np(ids32), ids_on_got)
+    np.testing.assert_array_equal(to_np(ids64), ids_on_got.astype(np.int64))
+    np.testing.assert_allclose(to_np(weights), w_on_got, rtol=2e-6, atol=2e-6)
+    # And equal to the oracle's routing on exact logits wherever the margin is not a near-tie.
+    ids_ref, _, _ = oracle.topk_route(ref_logits, to_np(bias), topk)
+    safe = route_margin(ref_logits, to_np(bias), topk) > 1e-4
+    np.testing.assert_array_equal(np.sort(to_np(ids32)[safe], 1), np.sort(ids_ref[safe], 1))
