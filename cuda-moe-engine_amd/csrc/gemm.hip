@@ -41,6 +41,7 @@ struct GemmParams {
     int64_t nb;               // rows of one expert's B
     int64_t n_out;            // output columns (N, or I for gate/up)
     int64_t ldc;
+    int64_t rows;             // rows of A and C; spans are clamped to it
     int experts;
     int n_tiles;              // output column tiles
 };
@@ -88,7 +89,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
     const int n_tile = rel / m_tiles;
     const int m_tile = rel - n_tile * m_tiles;
     const int64_t row0 = offs[expert] + static_cast<int64_t>(m_tile) * BM;
-    const int64_t row_end = offs[expert + 1];
+    const int64_t row_end = min(static_cast<int64_t>(offs[expert + 1]), p.rows);
+    if (row0 < 0 || row0 >= row_end) return;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -267,6 +269,7 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
 int launch_grouped_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, const int32_t* offsets,
                         int64_t rows, int64_t n, int64_t k, int experts, hipStream_t stream) {
     GemmParams p{};
+    p.rows = rows;
     p.a = a;
     p.b = b;
     p.c = c;
@@ -283,6 +286,7 @@ int launch_gateup_swiglu(const uint16_t* a, const uint16_t* gate_up, uint16_t* a
                          const int32_t* offsets, int64_t rows, int64_t hidden,
                          int64_t intermediate, int experts, hipStream_t stream) {
     GemmParams p{};
+    p.rows = rows;
     p.a = a;
     p.b = gate_up;
     p.c = act;
