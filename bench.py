@@ -1,0 +1,276 @@
+"""MoE block forward benchmark on one MI355X (implementation="cuda_fused").
+
+Workload (BASELINE metric configuration): H=4096, I=14336, E=8, top-2,
+T=4096 tokens, bf16 x ~ N(0,1), random-init weights of that architecture
+(router fp32 ~ N(0,1/H), gate_up/down bf16 ~ N(0,1/fan_in)), zero router bias.
+Inputs and weights are resident in HBM before timing starts.
+
+Prints ONE JSON line: value = mean forward latency (us) over the timed steps,
+plus per-stage latencies, expert-GEMM TFLOP/s, dispatch/combine GB/s, the
+roofline of the dominant kernel (gate/up GEMM with the SwiGLU epilogue, timed
+with events on the stream it is launched on), the PyTorch variant on the same
+GPU, and a CPU baseline (the oracle on a bounded token sample, rank 0 only).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "cuda-moe-engine_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+CONFIGS = {
+    # name: (tokens, hidden, intermediate, experts, topk, pattern)
+    "c4_t4096": (4096, 4096, 14336, 8, 2, "balanced"),
+    "c4_t16": (16, 4096, 14336, 8, 2, "balanced"),
+    "c4_t1": (1, 4096, 14336, 8, 2, "balanced"),
+    "c1": (128, 512, 1024, 8, 2, "balanced"),
+    "c3_t4096": (4096, 1024, 2048, 16, 2, "balanced"),
+    "c5": (8192, 2048, 1408, 64, 6, "zipf"),
+}
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c4_t4096", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch-variant", action="store_true")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=4)
+    return ap.parse_args(argv)
+
+
+def _events(n):
+    import torch
+
+    return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+
+
+def time_stages(block, x, steps, warmup):
+    """Per-stage event timing; every event is recorded on the stream the kernels use."""
+    import torch
+
+    state = block.workspace(x)
+    stages = {}
+
+    def route():
+        stages["_route"] = block.route(x)
+
+    def dispatch():
+        ids32, ids64, _ = stages["_route"]
+        state.transport.dispatch(x, ids32, ids64)
+
+    ext = block._extension
+
+    def gateup():
+        ext.gateup_swiglu_out(state.transport.packed, block.gate_up_weight, state.transport.offsets,
+                              state.activated)
+
+    def down():
+        ext.grouped_gemm_out(state.activated, block.down_weight, state.transport.offsets,
+                             state.expert_output)
+
+    def combine():
+        state.transport.combine(state.expert_output, stages["_route"][2])
+
+    order = [("router", route), ("dispatch", dispatch), ("gateup_swiglu", gateup), ("down", down),
+             ("combine", combine)]
+    with torch.inference_mode():
+        for _ in range(warmup):
+            for _, fn in order:
+                fn()
+        torch.cuda.synchronize()
+        ev = {name: _events(steps) for name, _ in order}
+        for i in range(steps):
+            for name, fn in order:
+                s, e = ev[name][i]
+                s.record()
+                fn()
+                e.record()
+        torch.cuda.synchronize()
+    out = {}
+    for name, _ in order:
+        samples = [s.elapsed_time(e) * 1000.0 for s, e in ev[name]]
+        out[name] = {"mean_us": statistics.fmean(samples), "median_us": statistics.median(samples),
+                     "min_us": min(samples)}
+    return out
+
+
+def cpu_baseline(block, x, sample_tokens):
+    """The CPU oracle on `sample_tokens` tokens of the same workload; scaled to a full forward."""
+    import numpy as np
+
+    from oracle import moe_oracle as oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    tokens = x.shape[0]
+    sample = x[:sample_tokens].float().cpu().numpy()
+    router = block.router_weight.cpu().numpy()
+    bias = block.routing_bias.cpu().numpy()
+    cfg = block.config
+    t0 = time.perf_counter()
+    logits = oracle.router_logits(sample, router)
+    ids, weights, _ = oracle.topk_route(logits, bias, cfg.topk)
+    used = sorted(set(ids.reshape(-1).tolist()))
+    gate_up = {e: block.gate_up_weight[e].float().cpu().numpy() for e in used}
+    down = {e: block.down_weight[e].float().cpu().numpy() for e in used}
+    convert_s = time.perf_counter() - t0
+
+    class _W:
+        def __init__(self, d, shape):
+            self.d, self.shape = d, shape
+
+        def __getitem__(self, e):
+            return self.d[e]
+
+    t1 = time.perf_counter()
+    oracle.token_major_forward(sample, _W(gate_up, tuple(block.gate_up_weight.shape)),
+                               _W(down, tuple(block.down_weight.shape)), ids, weights)
+    compute_s = time.perf_counter() - t1 + (t1 - t0 - convert_s)
+    per_token_us = compute_s * 1e6 / sample_tokens
+    return {
+        "value": per_token_us * tokens,
+        "unit": "us",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{sample_tokens} of {tokens} tokens through the numpy oracle (router, top-k, "
+                  f"per-expert float64 GEMMs, SwiGLU, combine); {compute_s:.2f} s, scaled x{tokens / sample_tokens:.0f}",
+    }
+
+
+def torch_variant_gpu(cfg, weights, x, steps, warmup):
+    import torch
+
+    from moe_dispatch.benchmark import measure
+    from moe_dispatch.experts import torch_backend_kind
+    from moe_dispatch.layer import MoEBlock
+
+    block = MoEBlock(cfg, device=x.device, implementation="torch", expert_backend="torch", weights=weights)
+    kind = torch_backend_kind(x.device)
+    stats = measure(lambda: block(x), warmup, steps)
+    del block
+    torch.cuda.empty_cache()
+    return {"median_us": stats["median_us"], "min_us": stats["min_us"], "gemm_backend": kind}
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are out of scope",
+                          "n_gpus": args.gpus}))
+        return 2
+    import numpy as np
+    import torch
+
+    from moe_dispatch.layer import MoEBlock, MoEConfig, MoEWeights, make_weights
+    from oracle import moe_oracle as oracle
+
+    tokens, hidden, inter, experts, topk, pattern = CONFIGS[args.config]
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    cfg = MoEConfig(hidden, inter, experts, topk)
+    weights = make_weights(cfg, device, torch.bfloat16, seed=0)
+    block = MoEBlock(cfg, device=device, implementation="cuda_fused", weights=weights)
+    if pattern == "zipf":
+        block.set_routing_bias(torch.from_numpy(oracle.zipf_bias(experts)))
+    gen = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(tokens, hidden, device=device, generator=gen).bfloat16()
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            block(x)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        per_step = _events(args.steps)
+        start.record()
+        for i in range(args.steps):
+            per_step[i][0].record()
+            block(x)
+            per_step[i][1].record()
+        end.record()
+        torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    step_us = [s.elapsed_time(e) * 1000.0 for s, e in per_step]
+    mean_us = total_ms * 1000.0 / args.steps
+
+    stages = time_stages(block, x, args.steps, min(args.warmup, 3))
+    counts = block.workspace(x).transport.counts.cpu().numpy()
+    offsets = block.workspace(x).transport.offsets.cpu().numpy()
+    n_assign = tokens * topk
+    pad_rows = int(offsets[-1]) - n_assign
+    gateup_flop = 4.0 * n_assign * hidden * inter
+    down_flop = 2.0 * n_assign * hidden * inter
+    t_gu = stages["gateup_swiglu"]["mean_us"]
+    t_dn = stages["down"]["mean_us"]
+    expert_tflops = (gateup_flop + down_flop) / ((t_gu + t_dn) * 1e-6) / 1e12
+    disp_bytes = oracle.dispatch_bytes(tokens, hidden, topk, pad_rows)
+    comb_bytes = oracle.combine_bytes(tokens, hidden, topk)
+    gu_tflops = gateup_flop / (t_gu * 1e-6) / 1e12
+
+    result = {
+        "metric": "MoE block fwd latency (us) + expert TFLOP/s % bf16 MFMA peak; dispatch GB/s",
+        "value": round(mean_us, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_us / 1000.0, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, random-init weights of the named shape)",
+        "config": {"workload": f"MoE block fwd {args.config}: T={tokens} H={hidden} I={inter} E={experts} "
+                               f"top-{topk} {pattern} routing, implementation=cuda_fused",
+                   "tokens": tokens, "hidden": hidden, "intermediate": inter, "experts": experts,
+                   "topk": topk, "alignment": cfg.alignment},
+        "median_step_us": round(statistics.median(step_us), 2),
+        "stages_us": {k: round(v["mean_us"], 2) for k, v in stages.items()},
+        "expert_tflops": round(expert_tflops, 1),
+        "expert_mfma_frac": round(expert_tflops / BF16_PEAK_TFLOPS, 4),
+        "dispatch_gbs": round(disp_bytes / (stages["dispatch"]["mean_us"] * 1e-6) / 1e9, 1),
+        "combine_gbs": round(comb_bytes / (stages["combine"]["mean_us"] * 1e-6) / 1e9, 1),
+        "expert_counts": counts.tolist(),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "grouped_gemm_kernel<SWIGLU> (gate/up + SwiGLU)",
+            "achieved": round(gu_tflops, 1),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gu_tflops / BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "flop_per_launch": gateup_flop,
+            "avg_launch_us": round(t_gu, 2),
+        },
+    }
+    if not args.no_torch_variant:
+        try:
+            result["torch_variant_gpu_us"] = torch_variant_gpu(cfg, weights, x, min(args.steps, 10), 2)
+        except RuntimeError as exc:  # e.g. out of memory: report, do not hide
+            result["torch_variant_gpu_us"] = {"error": str(exc)[:200]}
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(block, x, args.cpu_sample_tokens)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,66 @@
+"""The C-ABI library loads and exports every entry point include/moe_hip.h declares.
+
+Argument validation runs before any HIP call, so the error paths are checked
+here without a GPU (no kernel is launched).
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from moe_dispatch import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "moe_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    assert declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load_library()
+    handle = ctypes.CDLL(str(lib.path))
+    for name in declared_functions():
+        assert hasattr(handle, name), name
+    assert lib.moe_abi_version() == _lib.ABI_VERSION
+
+
+def test_status_strings():
+    lib = _lib.load_library()
+    assert lib.moe_status_string(0) == b"ok"
+    assert lib.moe_status_string(4) == b"workspace too small"
+    assert lib.moe_status_string(99) == b"unknown status"
+
+
+def test_validation_errors_without_launching():
+    lib = _lib.load_library()
+    assert lib.moe_topk_route(None, None, None, None, None, 5, 65, 2, None) == 2
+    assert b"1..64" in lib.moe_last_error()
+    assert lib.moe_topk_route(None, None, None, None, None, 5, 8, 9, None) == 2
+    # Empty batches are valid no-ops.
+    assert lib.moe_topk_route(None, None, None, None, None, 0, 8, 2, None) == 0
+    assert lib.moe_combine(None, 2, None, None, None, 0, 64, 2, 0, None) == 0
+    # Undersized packed workspace: T=10, K=2, E=8, a=8 needs 80 rows.
+    need = lib.moe_dispatch_scratch_bytes(10, 8, 2)
+    assert need > 0
+    status = lib.moe_dispatch(1, 2, 1, 1, 1, 1, 1, 1, 1, need, 10, 64, 8, 2, 8, 79, 1, None)
+    assert status == 4 and b"needs 80" in lib.moe_last_error()
+    assert lib.moe_dispatch(1, 2, 1, 1, 1, 1, 1, 1, 1, 0, 10, 64, 8, 2, 8, 80, 1, None) == 4
+    assert lib.moe_dispatch(1, 7, 1, 1, 1, 1, 1, 1, 1, need, 10, 64, 8, 2, 8, 80, 1, None) == 1
+    assert lib.moe_grouped_gemm(1, 1, 1, 1, 16, 12, 64, 8, None) == 2
+    assert lib.moe_grouped_gateup_swiglu(1, 1, 1, 1, 16, 64, 64, 65, None) == 2
+    assert lib.moe_router_fused(1, 1, 1, 1, 1, 1, None, 4, 12, 8, 2, None) == 2
+
+
+def test_error_surfaces_as_runtime_error():
+    lib = _lib.load_library()
+    with pytest.raises(_lib.MoeHipError, match="1..64"):
+        lib.check(lib.moe_topk_route(None, None, None, None, None, 5, 65, 2, None), "topk")
