@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const typename Elem<DT>::T*
         const int64_t base = r * width * 2 + c;
         const float g = Elem<DT>::load(proj[base]);
         const float u = Elem<DT>::load(proj[base + width]);
-        out[i] = Elem<DT>::store((g / (1.0f + expf(-g))) * u);
+        out[i] = Elem<DT>::store(silu_f32(g) * u);
     }
 }
 

@@ -48,8 +48,6 @@ struct GemmParams {
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
-
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p) {
     constexpr int WTM = BM / WAVES_M;
@@ -226,7 +224,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
                     if (grow < row_end) {
                         const float g = bf16_to_f32(f32_to_bf16(acc[i][j][r]));
                         const float u = bf16_to_f32(f32_to_bf16(acc[i][j + HALF_SN][r]));
-                        p.c[grow * p.ldc + col] = f32_to_bf16(silu(g) * u);
+                        p.c[grow * p.ldc + col] = f32_to_bf16(silu_f32(g) * u);
                     }
                 }
             }

@@ -61,6 +61,39 @@ template <> struct Elem<MOE_DTYPE_BF16> {
     static __device__ __forceinline__ T store(float f) { return f32_to_bf16(f); }
 };
 
+// ---------------------------------------------------------------------------
+// exp and SiLU with a fixed operation sequence, so a CPU restatement with
+// IEEE fp32 operations reproduces them bit for bit: Cody-Waite reduction
+// x = n*ln2 + r (ln2 = 16-bit head + tail, so n*ln2_hi is exact), degree-7
+// Taylor polynomial of e^r in Horner form with separately rounded multiply and
+// add, then ldexp. Within 2 ulp of exp on [-80, 88]; +inf above, 0 below
+// (where 1 + e^x already rounds to 1).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float exp_f32(float x) {
+#pragma clang fp contract(off)
+    if (x != x) return x;
+    if (x > 88.0f) return __builtin_inff();
+    if (x < -80.0f) return 0.0f;
+    const float n = rintf(x * __uint_as_float(0x3fb8aa3bu));  // log2(e)
+    float r = x - n * __uint_as_float(0x3f317200u);            // ln2 head
+    r = r - n * __uint_as_float(0x35bfbe8eu);                  // ln2 tail
+    float p = __uint_as_float(0x39500d01u);                    // 1/7!
+    p = p * r + __uint_as_float(0x3ab60b61u);                  // 1/6!
+    p = p * r + __uint_as_float(0x3c088889u);                  // 1/5!
+    p = p * r + __uint_as_float(0x3d2aaaabu);                  // 1/4!
+    p = p * r + __uint_as_float(0x3e2aaaabu);                  // 1/3!
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, static_cast<int>(n));
+}
+
+// silu(g) = g / (1 + exp(-g)) with a correctly rounded fp32 division.
+__device__ __forceinline__ float silu_f32(float g) {
+#pragma clang fp contract(off)
+    return g / (1.0f + exp_f32(-g));
+}
+
 inline int dtype_size(int dtype) {
     switch (dtype) {
         case MOE_DTYPE_F32: return 4;

@@ -34,9 +34,13 @@ Pinning (what checks each function; see tests/test_oracle.py)
   every invariant of the reference's ``validate_case``.
 * ``pack``/``combine``: ``index_select`` identities and torch's fp32
   ``(y * w).sum(1)`` (bit-exact for K <= 2).
-* ``swiglu``: torch ``F.silu`` in fp32 then one bf16 cast (reference
+* ``exp_f32``/``silu_f32``/``swiglu``: float64 ``exp`` (within 2 ulp over the
+  whole domain), torch ``F.silu`` in fp32 then one bf16 cast (reference
   ``experts.py:38-41``).
-* ``grouped_gemm``: a per-expert ``torch.matmul`` in float64.
+* ``grouped_gemm``: a per-expert ``torch.matmul`` in float64 ("exact" order,
+  and the "mfma" order within the fp32 error bound of it); the "mfma" order
+  against a pure-Python loop over k-groups on tiny inputs; on the GPU the
+  kernels match the "mfma" order bit for bit.
 * ``block_forward``: the restated ``token_major_oracle`` (dense, token-major,
   independent of the permutation).
 """
@@ -60,6 +64,8 @@ __all__ = [
     "combine",
     "swiglu",
     "grouped_gemm",
+    "exp_f32",
+    "silu_f32",
     "block_forward",
     "token_major_forward",
     "zipf_bias",
@@ -259,29 +265,101 @@ def pack(x: np.ndarray, layout: dict, topk: int, rows: int):
 # ----------------------------------------------------------------------------
 
 
-def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray) -> np.ndarray:
-    """Grouped GEMM ``C[r] = A[r] @ B[e]^T`` for rows r of expert e.
+def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray, order: str = "mfma") -> np.ndarray:
+    """Grouped GEMM ``C[r] = A[r] @ B[e]^T`` for rows r of expert e, fp32 result.
 
     Reference ``experts.py:21-35`` with ``ENDS = offsets[1:]`` and the masked
-    row groups of ``_triton_gemm.py:27-70``. Accumulates in float64 and returns
-    float32 (unrounded). Rows at or past ``offsets[E]`` are returned as 0 and
-    are undefined for the kernels.
+    row groups of ``_triton_gemm.py:27-70`` (fp32 accumulation; the order of the
+    fp32 additions is not specified there). Two orders:
+
+    * ``"exact"``: float64 accumulation, one rounding to fp32 (the correctly
+      rounded dot product);
+    * ``"mfma"`` (default): the accumulation order of the HIP kernels, which
+      apply ``v_mfma_f32_32x32x16_bf16`` along k in ascending order. That
+      instruction adds each ascending group of 8 products, summed exactly, to
+      the fp32 accumulator with one round-to-nearest-even. Measured on MI355X:
+      this model reproduces the kernel's outputs bit for bit (K=14336), while
+      the exact dot product differs in ~0.05% of bf16 outputs.
+
+    Rows at or past ``offsets[E]`` are returned as 0 (undefined for the kernels).
     """
+    if order not in ("mfma", "exact"):
+        raise ValueError("order must be 'mfma' or 'exact'")
     a64 = np.asarray(a, dtype=np.float64)
-    out = np.zeros((a64.shape[0], b.shape[1]), dtype=np.float64)
+    out = np.zeros((a64.shape[0], b.shape[1]), dtype=np.float32)
     offsets = np.asarray(offsets, dtype=np.int64)
     for e in range(b.shape[0]):
         s, t = int(offsets[e]), int(offsets[e + 1])
-        if t > s:
-            out[s:t] = a64[s:t] @ np.asarray(b[e], dtype=np.float64).T
-    return out.astype(np.float32)
+        if t <= s:
+            continue
+        be = np.asarray(b[e], dtype=np.float64)
+        if order == "exact":
+            out[s:t] = (a64[s:t] @ be.T).astype(np.float32)
+        else:
+            out[s:t] = _mfma_order_matmul(a64[s:t], be)
+    return out
+
+
+def _mfma_order_matmul(a64: np.ndarray, b64: np.ndarray, group: int = 8) -> np.ndarray:
+    """``a @ b.T`` accumulated as: acc = fp32(acc + exact sum of k-group), groups ascending."""
+    m, k = a64.shape
+    n = b64.shape[0]
+    pad = (-k) % group
+    if pad:
+        a64 = np.pad(a64, ((0, 0), (0, pad)))
+        b64 = np.pad(b64, ((0, 0), (0, pad)))
+    groups = a64.shape[1] // group
+    ag = a64.reshape(m, groups, group).transpose(1, 0, 2)  # [G, m, 8]
+    bg = b64.reshape(n, groups, group).transpose(1, 2, 0)  # [G, 8, n]
+    acc = np.zeros((m, n), dtype=np.float32)
+    col_block = max(1, (1 << 24) // max(1, m * 64))
+    for c0 in range(0, n, col_block):
+        c1 = min(n, c0 + col_block)
+        part = np.zeros((m, c1 - c0), dtype=np.float32)
+        for g0 in range(0, groups, 64):
+            sums = np.matmul(ag[g0:g0 + 64], bg[g0:g0 + 64, :, c0:c1])  # exact group sums
+            for i in range(sums.shape[0]):
+                part = (part.astype(np.float64) + sums[i]).astype(np.float32)
+        acc[:, c0:c1] = part
+    return acc
+
+
+# exp for SiLU, reproducible bit for bit on the GPU: Cody-Waite range
+# reduction x = n*ln2 + r (ln2 split into a 16-bit head and a tail so n*ln2_hi is
+# exact), then the degree-7 Taylor polynomial of e^r in Horner form, every step
+# a separately rounded fp32 operation (no fused multiply-add), then 2^n scaling.
+# |r| <= ln2/2 gives a truncation error below 1e-8 relative; the result is
+# within 2 ulp of exp (checked against float64 exp in tests/test_oracle.py).
+EXP_LOG2E = np.float32(1.4426950216293335)        # 0x3fb8aa3b
+EXP_LN2_HI = np.float32(0.693145751953125)        # 0x3f317200
+EXP_LN2_LO = np.float32(1.428606765330187e-06)    # 0x35bfbe8e
+EXP_TAYLOR = tuple(np.float32(1.0 / math.factorial(k)) for k in range(7, -1, -1))
+EXP_MAX = np.float32(88.0)     # above: +inf
+EXP_MIN = np.float32(-80.0)    # below: 0 (1 + e^x rounds to 1 anyway)
+
+
+def exp_f32(x: np.ndarray) -> np.ndarray:
+    """fp32 exp with the kernels' exact operation sequence."""
+    x = np.asarray(x, dtype=np.float32)
+    n = np.rint((x * EXP_LOG2E).astype(np.float32)).astype(np.float32)
+    r = (x - (n * EXP_LN2_HI).astype(np.float32)).astype(np.float32)
+    r = (r - (n * EXP_LN2_LO).astype(np.float32)).astype(np.float32)
+    p = np.full_like(r, EXP_TAYLOR[0])
+    for c in EXP_TAYLOR[1:]:
+        p = ((p * r).astype(np.float32) + c).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        ni = np.where(np.isfinite(n), n, 0).astype(np.int32)
+    out = np.ldexp(p, ni).astype(np.float32)
+    out = np.where(x > EXP_MAX, np.float32(np.inf), out)
+    out = np.where(x < EXP_MIN, np.float32(0.0), out)
+    return np.where(np.isnan(x), x, out).astype(np.float32)
 
 
 def silu_f32(g: np.ndarray) -> np.ndarray:
-    """``g / (1 + exp(-g))`` in fp32 (reference ``csrc/dispatch.cu:288-291``)."""
+    """``g / (1 + exp(-g))`` in fp32 (reference ``csrc/dispatch.cu:288-291``), exp as ``exp_f32``."""
     g = np.asarray(g, dtype=np.float32)
-    with np.errstate(over="ignore"):
-        return (g / (np.float32(1.0) + np.exp(-g))).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (g / (np.float32(1.0) + exp_f32(-g))).astype(np.float32)
 
 
 def swiglu(projection: np.ndarray, valid_rows: int, dtype: str = "bf16") -> np.ndarray:
@@ -327,7 +405,7 @@ def combine(expert_output: np.ndarray, inverse: np.ndarray, weights: np.ndarray,
 
 
 def block_forward(x, router_w, bias, gate_up, down, topk, alignment=8, ids=None,
-                  weights=None):
+                  weights=None, gemm_order="mfma"):
     """Expert-major block forward with the kernels' rounding points.
 
     Restates ``MoEBlock.forward`` for ``implementation="cuda_fused"``
@@ -335,8 +413,9 @@ def block_forward(x, router_w, bias, gate_up, down, topk, alignment=8, ids=None,
     (bf16 projection) -> SwiGLU (bf16) -> down GEMM (bf16) -> combine (bf16).
 
     ``x`` holds bf16 values (float32 array). ``ids``/``weights`` may be given to
-    evaluate the downstream stages on a fixed routing. Returns a dict of every
-    intermediate.
+    evaluate the downstream stages on a fixed routing. ``gemm_order`` selects
+    the fp32 accumulation order of the GEMMs (see ``grouped_gemm``). Returns a
+    dict of every intermediate.
     """
     x = np.asarray(x, dtype=np.float32)
     tokens, hidden = x.shape
@@ -348,9 +427,9 @@ def block_forward(x, router_w, bias, gate_up, down, topk, alignment=8, ids=None,
     rows = capacity_rows(tokens, experts, topk, alignment)
     packed, _ = pack(x, layout, topk, rows)
     offsets = layout["offsets"]
-    projection = bf16_round(grouped_gemm(packed, gate_up, offsets))
+    projection = bf16_round(grouped_gemm(packed, gate_up, offsets, order=gemm_order))
     activated = swiglu(projection, int(offsets[-1]))
-    expert_output = bf16_round(grouped_gemm(activated, down, offsets))
+    expert_output = bf16_round(grouped_gemm(activated, down, offsets, order=gemm_order))
     output = combine(expert_output, layout["inverse"], weights)
     return {
         "logits": logits,
@@ -366,7 +445,7 @@ def block_forward(x, router_w, bias, gate_up, down, topk, alignment=8, ids=None,
     }
 
 
-def token_major_forward(x, gate_up, down, ids, weights, token_index=None):
+def token_major_forward(x, gate_up, down, ids, weights, token_index=None, order="exact"):
     """Dense token-major evaluation (reference ``layer.py:200-214``).
 
     Independent of dispatch: for each expert, evaluates every (selected) token
@@ -374,6 +453,8 @@ def token_major_forward(x, gate_up, down, ids, weights, token_index=None):
     rounds once. Projection, activation and expert output are rounded to bf16
     as the reference's ``F.linear`` on bf16 tensors does. ``token_index``
     restricts the evaluation to a subset of tokens (for full-size samples).
+    ``order`` is the fp32 accumulation order of the dot products ("exact":
+    float64 then one rounding; "mfma": see ``grouped_gemm``).
     """
     x = np.asarray(x, dtype=np.float32)
     ids = np.asarray(ids)
@@ -391,9 +472,10 @@ def token_major_forward(x, gate_up, down, ids, weights, token_index=None):
         rows = np.nonzero(probability)[0]
         if rows.size == 0:
             continue
-        proj = bf16_round((x[rows].astype(np.float64) @ np.asarray(gate_up[e], np.float64).T).astype(np.float32))
+        one = np.array([0, rows.size])
+        proj = bf16_round(grouped_gemm(x[rows], np.asarray(gate_up[e])[None], one, order=order))
         act = bf16_round((silu_f32(proj[:, :width]) * proj[:, width:]).astype(np.float32))
-        out = bf16_round((act.astype(np.float64) @ np.asarray(down[e], np.float64).T).astype(np.float32))
+        out = bf16_round(grouped_gemm(act, np.asarray(down[e])[None], one, order=order))
         expected[rows] = (expected[rows] + out * probability[rows, None]).astype(np.float32)
     return bf16_round(expected)
 

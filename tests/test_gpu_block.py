@@ -6,9 +6,15 @@ For each configuration the test checks, in order:
     products in its own order); the downstream oracle then uses the kernel's
     routing so the remaining stages are compared on identical inputs;
   * dispatch: counts, offsets and inverse bit-exact, packed rows bit-exact;
-  * output: max-abs <= 1.6e-2 and relative L2 <= 5e-4 against the expert-major
-    oracle (bf16 rounding at projection, activation, expert output, output),
-    and against the independent token-major oracle.
+  * activation, expert output and block output: bit-exact against the
+    expert-major oracle (MFMA-order fp32 accumulation, bf16 rounding at
+    projection, activation, expert output and output), so max-abs 0 and
+    relative L2 0 (north-star bound: 1.6e-2 / 5e-4);
+  * independently, the token-major oracle with exact float64 dot products:
+    max-abs <= 1.6e-2 and relative L2 <= 5e-4 at the small and medium shapes;
+    at I=14336 the bound is 2e-3 (two fp32 summation orders disagree there by
+    ~1e-3: a few 1-ulp bf16 flips of the activation perturb every expert
+    output element, which flips ~6% of their bf16 roundings).
 The reference's own gate (tests/test_gpu.py:43-48 -> block_benchmark.check_forward,
 rtol = atol = 3e-2, rel-L2 <= 2e-2) is implied by these bounds.
 """
@@ -25,6 +31,7 @@ pytestmark = gpu
 
 MAX_ABS = 1.6e-2
 REL_L2 = 5e-4
+REL_L2_LARGE_I = 2e-3  # exact-arithmetic comparison at I=14336 (see module docstring)
 
 
 def _run_block(cfg, tokens, pattern, seed, bias=None):
@@ -66,12 +73,11 @@ def _check_block(cfg, tokens, pattern="balanced", seed=0, bias=None):
     np.testing.assert_array_equal(to_np(transport.inverse), layout["inverse"])
     used = int(layout["offsets"][-1])
     np.testing.assert_array_equal(to_np(transport.packed)[:used], ref["packed"][:used])
+    np.testing.assert_array_equal(to_np(state.activated)[:used], ref["activated"][:used])
+    np.testing.assert_array_equal(to_np(state.expert_output)[:used], ref["expert_output"][:used])
     got = to_np(out)
-    expect = ref["output"]
-    max_abs = float(np.abs(got - expect).max()) if got.size else 0.0
-    rel = rel_l2(got, expect)
-    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
-    dense = oracle.token_major_forward(xf, gate_up, down, ids, w)
+    np.testing.assert_array_equal(got, ref["output"])
+    dense = oracle.token_major_forward(xf, gate_up, down, ids, w, order="exact")
     assert float(np.abs(got - dense).max()) <= MAX_ABS
     assert rel_l2(got, dense) <= REL_L2
     return layout["counts"]
@@ -143,11 +149,14 @@ def test_config4_decode_sizes_full_model_shape(tokens):
     cfg = MoEConfig(4096, 14336, 8, 2)
     block, x, out, ids32, weights, state = _run_block(cfg, tokens, "balanced", seed=1)
     ids, w = to_np(ids32), to_np(weights)
-    dense = oracle.token_major_forward(
-        to_np(x), LazyExpertWeights(block.gate_up_weight), LazyExpertWeights(block.down_weight), ids, w
-    )
+    gate_up, down = LazyExpertWeights(block.gate_up_weight), LazyExpertWeights(block.down_weight)
     got = to_np(out)
+    # Bit-exact against the token-major oracle with the kernels' accumulation order (K=2:
+    # the expert-order and k-order fp32 sums of two terms are the same number).
+    same_order = oracle.token_major_forward(to_np(x), gate_up, down, ids, w, order="mfma")
+    np.testing.assert_array_equal(got, same_order)
+    dense = oracle.token_major_forward(to_np(x), gate_up, down, ids, w, order="exact")
     assert float(np.abs(got - dense).max()) <= MAX_ABS
-    assert rel_l2(got, dense) <= REL_L2
+    assert rel_l2(got, dense) <= REL_L2_LARGE_I
     del block
     torch.cuda.empty_cache()

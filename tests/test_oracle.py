@@ -237,7 +237,7 @@ def test_grouped_gemm_matches_per_expert_torch_matmul():
     offsets = np.array([0, 8, 8, 40, 48], np.int32)
     a = torch.randn(50, 32, generator=g)
     b = torch.randn(4, 24, 32, generator=g)
-    got = oracle.grouped_gemm(a.numpy(), b.numpy(), offsets)
+    got = oracle.grouped_gemm(a.numpy(), b.numpy(), offsets, order="exact")
     for e in range(4):
         s, t = offsets[e], offsets[e + 1]
         np.testing.assert_allclose(got[s:t], (a[s:t].double() @ b[e].double().T).float().numpy(), rtol=1e-6)
@@ -287,3 +287,61 @@ def test_all_permutations_tiny_brute_force():
             counts, offsets, slots, inverse = _brute_layout(ids, 3, alignment)
             assert layout["inverse"].reshape(-1).tolist() == inverse
             assert layout["offsets"].tolist() == offsets
+
+
+# --------------------------------------------------------------------------- exp / MFMA order
+def _ulp_error(got, ref64):
+    ref32 = ref64.astype(np.float32)
+    spacing = np.spacing(np.abs(ref32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - ref64) / spacing
+
+
+def test_exp_f32_within_two_ulp_of_float64_exp():
+    x = np.concatenate([np.linspace(-80, 88, 2_000_003, dtype=np.float32),
+                        np.random.default_rng(0).uniform(-20, 20, 200_000).astype(np.float32)])
+    got = oracle.exp_f32(x)
+    err = _ulp_error(got, np.exp(x.astype(np.float64)))
+    assert err.max() <= 2.0, err.max()
+    assert np.mean(err <= 0.5) > 0.5
+
+
+def test_exp_f32_special_values():
+    x = np.array([0.0, -0.0, 88.5, 1e30, -80.5, -1e30, np.inf, -np.inf, np.nan], np.float32)
+    got = oracle.exp_f32(x)
+    assert got[0] == 1.0 and got[1] == 1.0
+    assert np.isinf(got[2]) and np.isinf(got[3]) and np.isinf(got[6])
+    assert got[4] == 0.0 and got[5] == 0.0 and got[7] == 0.0
+    assert np.isnan(got[8])
+
+
+def test_silu_f32_matches_torch_silu():
+    g = np.random.default_rng(1).standard_normal(100_000).astype(np.float32) * 6
+    got = oracle.silu_f32(g)
+    ref = torch.nn.functional.silu(torch.from_numpy(g).double()).numpy()
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 4e-7
+
+
+def test_mfma_order_matches_python_loop_definition():
+    rng = np.random.default_rng(3)
+    a = oracle.bf16_round(rng.standard_normal((3, 40)).astype(np.float32))
+    b = oracle.bf16_round(rng.standard_normal((1, 5, 40)).astype(np.float32))
+    got = oracle.grouped_gemm(a, b, np.array([0, 3]), order="mfma")
+    for i in range(3):
+        for j in range(5):
+            acc = np.float32(0.0)
+            for g0 in range(0, 40, 8):
+                exact = sum(float(a[i, k]) * float(b[0, j, k]) for k in range(g0, g0 + 8))
+                acc = np.float32(float(acc) + exact)
+            assert got[i, j] == acc
+
+
+def test_mfma_order_is_within_fp32_bound_of_exact():
+    rng = np.random.default_rng(4)
+    a = oracle.bf16_round(rng.standard_normal((64, 1024)).astype(np.float32))
+    b = oracle.bf16_round((rng.standard_normal((2, 96, 1024)) / 32).astype(np.float32))
+    offsets = np.array([0, 30, 64])
+    mfma = oracle.grouped_gemm(a, b, offsets, order="mfma")
+    exact = oracle.grouped_gemm(a, b, offsets, order="exact")
+    bound = 128 * np.finfo(np.float32).eps * (np.abs(a) @ np.abs(b[0]).T).max()
+    assert np.max(np.abs(mfma - exact)) <= bound
+    assert np.any(mfma != exact)  # the orders do differ somewhere
