@@ -247,6 +247,232 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 }
 
 // ---------------------------------------------------------------------------
+// Fast path (K % 64 == 0): 256 x 256 x 64 tiles fed by direct-to-LDS buffer
+// loads (buffer_load_dwordx4 ... lds). Each wavefront load moves 8 LDS rows
+// (1 KiB); lane l lands at byte 16*l of that block, i.e. row l/8, physical
+// chunk l%8, so it fetches logical chunk (l%8) ^ (l/8) of its row to realise
+// the XOR swizzle. Buffer resources bound the valid bytes: rows past the
+// expert's span and weight rows past the expert read as zero without
+// per-lane predicates. The last row tile of an expert is 64, 128 or 256 rows
+// high (the smallest that holds the remainder), so skewed and ragged spans do
+// not pay for a full 256-row tile. The k order of the MFMA chain (ascending,
+// one accumulator) is the same as the generic path.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format
+constexpr int kFastStage = (256 + 256) * kBK;  // bf16 elements per LDS stage (A then B)
+
+// Resource descriptor from wave-uniform values, pinned to SGPRs with readfirstlane
+// so buffer instructions take it directly (no waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
+    void* uniform_base = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(uniform_base, 0, __builtin_amdgcn_readfirstlane(bytes),
+                                             kRsrcWord3);
+}
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint16_t* lds_dst, uint32_t voffset,
+                                      uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rsrc, (__attribute__((address_space(3))) void*)(lds_dst), 16, voffset, soffset,
+        0, 0);
+}
+
+template <int SMT, bool SWIGLU>
+__device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, int expert, int n_tile,
+                                          int64_t row0, int64_t row_end) {
+    constexpr int TM = SMT * 64;        // rows of this tile (2 wave rows x SMT x 32)
+    constexpr int WTM = TM / 2;
+    constexpr int WTN = 128;
+    constexpr int SN = 4;
+    constexpr int A_LOADS = TM / 32;    // 8-row wavefront loads per wave
+    constexpr int B_LOADS = 8;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int64_t K = p.k;
+
+    const int64_t a_rows = min<int64_t>(row_end - row0, TM);
+    const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(p.a + row0 * K, static_cast<uint32_t>(a_rows * K * 2));
+    const __amdgpu_buffer_rsrc_t rsrc_b =
+        make_rsrc(p.b + static_cast<int64_t>(expert) * p.nb * K, static_cast<uint32_t>(p.nb * K * 2));
+
+    const int lrow = lane >> 3;
+    const int lchunk = (lane & 7) ^ lrow;
+    uint32_t a_off[A_LOADS], b_off[B_LOADS];
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+        const int r = (wave * A_LOADS + i) * 8 + lrow;
+        a_off[i] = static_cast<uint32_t>((r * K + lchunk * 8) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+        const int r = (wave * B_LOADS + i) * 8 + lrow;
+        int64_t brow;
+        if constexpr (SWIGLU) {
+            const int wcol = r / WTN, w = r % WTN;
+            constexpr int HALF = WTN / 2;
+            const int64_t col = static_cast<int64_t>(n_tile) * 128 + wcol * HALF + (w % HALF);
+            brow = (w < HALF) ? col : p.n_out + col;
+        } else {
+            brow = static_cast<int64_t>(n_tile) * 256 + r;
+        }
+        b_off[i] = static_cast<uint32_t>((brow * K + lchunk * 8) * 2);
+    }
+
+    auto issue = [&](int kt, int stage) {
+        const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2;
+        uint16_t* sa = lds + stage * kFastStage;
+        uint16_t* sb = sa + 256 * kBK;
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) dma16(rsrc_a, sa + (wave * A_LOADS + i) * 8 * kBK, a_off[i], koff);
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) dma16(rsrc_b, sb + (wave * B_LOADS + i) * 8 * kBK, b_off[i], koff);
+    };
+
+    floatx16 acc[SMT][SN];
+#pragma unroll
+    for (int i = 0; i < SMT; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int frag_row = lane & 31;
+    const int frag_half = lane >> 5;
+    const int k_steps = static_cast<int>(K / kBK);
+
+    // Fragment reads of one 16-wide k slice and the MFMAs that consume them.
+    auto read = [&](const uint16_t* sa, const uint16_t* sb, int kk, bf16x8_t (&fa)[SMT], bf16x8_t (&fb)[SN]) {
+        const int chunk = kk * 2 + frag_half;
+#pragma unroll
+        for (int i = 0; i < SMT; ++i) {
+            const int r = wm * WTM + i * 32 + frag_row;
+            fa[i] = *reinterpret_cast<const bf16x8_t*>(&sa[swz(r, chunk)]);
+        }
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            const int r = wn * WTN + j * 32 + frag_row;
+            fb[j] = *reinterpret_cast<const bf16x8_t*>(&sb[swz(r, chunk)]);
+        }
+    };
+    auto mma = [&](const bf16x8_t (&fa)[SMT], const bf16x8_t (&fb)[SN]) {
+#pragma unroll
+        for (int i = 0; i < SMT; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    };
+    // sched_barrier(0) fences keep each phase in place: the fragment reads of
+    // slice kk+1 are issued before the MFMAs of slice kk, so LDS latency hides
+    // under the matrix pipe and two fragment sets stay live.
+    auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+
+    bf16x8_t fa0[SMT], fb0[SN], fa1[SMT], fb1[SN];
+    issue(0, 0);
+    __syncthreads();
+    read(lds, lds + 256 * kBK, 0, fa0, fb0);
+    for (int kt = 0; kt < k_steps; ++kt) {
+        const int stage = kt & 1;
+        const uint16_t* sa = lds + stage * kFastStage;
+        const uint16_t* sb = sa + 256 * kBK;
+        const uint16_t* na = lds + (stage ^ 1) * kFastStage;
+        const uint16_t* nb = na + 256 * kBK;
+        // Next tile into the other stage (the last step reloads the final tile,
+        // keeping the body branch free; the copy is never read).
+        issue(min(kt + 1, k_steps - 1), stage ^ 1);
+        read(sa, sb, 1, fa1, fb1);
+        fence();
+        mma(fa0, fb0);
+        fence();
+        read(sa, sb, 2, fa0, fb0);
+        fence();
+        mma(fa1, fb1);
+        fence();
+        read(sa, sb, 3, fa1, fb1);
+        fence();
+        mma(fa0, fb0);
+        fence();
+        // All waves are done with this stage's fragments and the next stage has landed.
+        __syncthreads();
+        read(na, nb, 0, fa0, fb0);
+        fence();
+        mma(fa1, fb1);
+        fence();
+    }
+
+    const int col_in = lane & 31;
+    const int row_in = (lane >> 5) * 4;
+    if constexpr (SWIGLU) {
+#pragma unroll
+        for (int i = 0; i < SMT; ++i) {
+#pragma unroll
+            for (int j = 0; j < SN / 2; ++j) {
+                const int64_t col = static_cast<int64_t>(n_tile) * 128 + wn * (WTN / 2) + j * 32 + col_in;
+                if (col >= p.n_out) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t grow = row0 + wm * WTM + i * 32 + (r >> 2) * 8 + row_in + (r & 3);
+                    if (grow < row_end) {
+                        const float g = bf16_to_f32(f32_to_bf16(acc[i][j][r]));
+                        const float u = bf16_to_f32(f32_to_bf16(acc[i][j + SN / 2][r]));
+                        p.c[grow * p.ldc + col] = f32_to_bf16(silu_f32(g) * u);
+                    }
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < SMT; ++i) {
+#pragma unroll
+            for (int j = 0; j < SN; ++j) {
+                const int64_t col = static_cast<int64_t>(n_tile) * 256 + wn * WTN + j * 32 + col_in;
+                if (col >= p.n_out) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t grow = row0 + wm * WTM + i * 32 + (r >> 2) * 8 + row_in + (r & 3);
+                    if (grow < row_end) p.c[grow * p.ldc + col] = f32_to_bf16(acc[i][j][r]);
+                }
+            }
+        }
+    }
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(kGemmThreads) void grouped_gemm_fast_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * kFastStage];
+    const int32_t* __restrict__ offs = p.offsets;
+    int total = 0;
+    for (int e = 0; e < p.experts; ++e) total += ((offs[e + 1] - offs[e] + 255) / 256) * p.n_tiles;
+    const int per_xcd = (total + kNumXcd - 1) / kNumXcd;
+    const int slot = blockIdx.x / kNumXcd;
+    if (slot >= per_xcd) return;
+    const int tile = (blockIdx.x % kNumXcd) * per_xcd + slot;
+    if (tile >= total) return;
+    int expert = 0, base = 0, m_tiles = 0, span = 0;
+    for (; expert < p.experts; ++expert) {
+        span = offs[expert + 1] - offs[expert];
+        m_tiles = (span + 255) / 256;
+        const int t = m_tiles * p.n_tiles;
+        if (tile < base + t) break;
+        base += t;
+    }
+    const int rel = tile - base;
+    const int n_tile = rel / m_tiles;
+    const int m_tile = rel - n_tile * m_tiles;
+    const int64_t row0 = offs[expert] + static_cast<int64_t>(m_tile) * 256;
+    const int64_t row_end = min(static_cast<int64_t>(offs[expert + 1]), p.rows);
+    if (row0 < 0 || row0 >= row_end) return;
+    const int rem = span - m_tile * 256;  // rows left from this tile on
+    if (rem > 128) fast_tile<4, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
+    else if (rem > 64) fast_tile<2, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
+    else fast_tile<1, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
@@ -259,6 +485,11 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
     if (blocks == 0) return MOE_OK;
     if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
+    if (BM == 256 && BN == 256 && p.k % kBK == 0) {
+        hipLaunchKernelGGL((grouped_gemm_fast_kernel<SWIGLU>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(kGemmThreads), 0, stream, p);
+        return check_launch("grouped_gemm_fast_kernel");
+    }
     hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, SWIGLU>),
                        dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads), 0, stream, p);
     return check_launch("grouped_gemm_kernel");
