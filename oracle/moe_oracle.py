@@ -40,7 +40,8 @@ Pinning (what checks each function; see tests/test_oracle.py)
 * ``grouped_gemm``: a per-expert ``torch.matmul`` in float64 ("exact" order,
   and the "mfma" order within the fp32 error bound of it); the "mfma" order
   against a pure-Python loop over k-groups on tiny inputs; on the GPU the
-  kernels match the "mfma" order bit for bit.
+  kernels match the "mfma" order in >99.99% of bf16 outputs (the rest one
+  bf16 step away).
 * ``block_forward``: the restated ``token_major_oracle`` (dense, token-major,
   independent of the permutation).
 """
@@ -275,11 +276,14 @@ def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray, order: str =
     * ``"exact"``: float64 accumulation, one rounding to fp32 (the correctly
       rounded dot product);
     * ``"mfma"`` (default): the accumulation order of the HIP kernels, which
-      apply ``v_mfma_f32_32x32x16_bf16`` along k in ascending order. That
-      instruction adds each ascending group of 8 products, summed exactly, to
-      the fp32 accumulator with one round-to-nearest-even. Measured on MI355X:
-      this model reproduces the kernel's outputs bit for bit (K=14336), while
-      the exact dot product differs in ~0.05% of bf16 outputs.
+      apply ``v_mfma_f32_32x32x16_bf16`` along k in ascending order, modelled
+      as: add the exact sum of each ascending group of 8 products to the fp32
+      accumulator with one round-to-nearest-even. Measured on MI355X the
+      grouping and rounding are right (other groupings and orders are far
+      off), but the hardware sums the 8 products with a limited-width internal
+      alignment, so ~0.2% of single-instruction fp32 results differ by one
+      ulp; after the bf16 output rounding ~1e-5 of GEMM outputs are one bf16
+      step away from this model, versus ~5e-4 for the exact dot product.
 
     Rows at or past ``offsets[E]`` are returned as 0 (undefined for the kernels).
     """

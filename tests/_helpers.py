@@ -77,3 +77,35 @@ def assert_packed_equal(packed: torch.Tensor, x: torch.Tensor, layout, topk):
     used = int(layout["offsets"][-1])
     got = raw_bits(packed)[:used]
     np.testing.assert_array_equal(got, expected[:used])
+
+
+def bf16_step(values: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 values at the magnitude of ``values`` (2^(e-7) for |v| in [2^e, 2^(e+1)))."""
+    mag = np.abs(np.asarray(values, np.float64))
+    _, e = np.frexp(np.where(mag > 0, mag, 2.0**-126))
+    return np.ldexp(1.0, e - 8)
+
+
+def assert_near_bit_exact(got, ref, max_fraction=1e-4, max_steps=1.0):
+    """GEMM-derived bf16 outputs against the MFMA-order oracle, given identical inputs.
+
+    The oracle models each v_mfma_f32_32x32x16_bf16 as: add the exact sum of
+    each ascending group of 8 products to the fp32 accumulator with one
+    round-to-nearest-even. The hardware adds the 8 products with a
+    limited-width internal alignment, so on random data about 0.2% of single
+    MFMA fp32 results differ from the model by one fp32 ulp. After rounding to
+    bf16 that leaves about 1e-5 of the outputs one bf16 step away. Requires
+    at most ``max_fraction`` of the elements to differ, each by at most
+    ``max_steps`` bf16 steps.
+    """
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    assert got.shape == ref.shape
+    differ = got != ref
+    if not differ.any():
+        return
+    fraction = differ.mean()
+    assert fraction <= max_fraction, f"{int(differ.sum())} of {got.size} elements differ ({fraction:.2e})"
+    step = bf16_step(np.maximum(np.abs(got[differ]), np.abs(ref[differ])))
+    worst = float(np.max(np.abs(got[differ].astype(np.float64) - ref[differ]) / step))
+    assert worst <= max_steps + 1e-9, f"largest difference is {worst:.2f} bf16 steps"
