@@ -14,7 +14,7 @@
 //    wave owns (BM/WAVES_M) x (BN/WAVES_N) as 32x32 MFMA sub-tiles; the fp32
 //    accumulators live in the AGPR/VGPR file (one wave per SIMD).
 //  * Global -> register -> LDS double buffering with one barrier per k-step.
-//    LDS rows are 128 bytes; 16-byte chunks are XOR-swizzled by (row & 7) so
+//    LDS rows are 128 bytes; 16-byte chunks are XOR-swizzled per row (swz) so
 //    both the 16-byte stores and the MFMA fragment reads are conflict free.
 //  * Tile schedule is built on the device from offsets: expert e contributes
 //    ceil(span_e/BM) x n_tiles tiles (0 for an empty expert). The grid is a
@@ -46,7 +46,13 @@ struct GemmParams {
     int n_tiles;              // output column tiles
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+// 16-byte chunk c of LDS row r lives at physical chunk c ^ f(r), f(r) = (r ^ (r >> 3)) & 7.
+// A 16-byte read is serviced 16 lanes at a time across 64 four-byte banks (two
+// 128-byte rows); with this f, 16 consecutive rows at one logical chunk hit 16
+// distinct (row parity, chunk) bank groups, so fragment reads are conflict free
+// (and so are 8-lane groups on a 32-bank LDS).
+__device__ __forceinline__ int swz_key(int row) { return (row ^ (row >> 3)) & 7; }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ swz_key(row)) << 3); }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p) {
@@ -250,8 +256,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 // Fast path (K % 64 == 0): 256 x 256 x 64 tiles fed by direct-to-LDS buffer
 // loads (buffer_load_dwordx4 ... lds). Each wavefront load moves 8 LDS rows
 // (1 KiB); lane l lands at byte 16*l of that block, i.e. row l/8, physical
-// chunk l%8, so it fetches logical chunk (l%8) ^ (l/8) of its row to realise
-// the XOR swizzle. Buffer resources bound the valid bytes: rows past the
+// chunk l%8, so it fetches the logical chunk that the swizzle maps there. Buffer resources bound the valid bytes: rows past the
 // expert's span and weight rows past the expert read as zero without
 // per-lane predicates. The last row tile of an expert is 64, 128 or 256 rows
 // high (the smallest that holds the remainder), so skewed and ragged spans do
@@ -300,17 +305,20 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
     const __amdgpu_buffer_rsrc_t rsrc_b =
         make_rsrc(p.b + static_cast<int64_t>(expert) * p.nb * K, static_cast<uint32_t>(p.nb * K * 2));
 
+    // Lane l of an 8-row wavefront load lands at row r0 + l/8, physical chunk l%8,
+    // so it fetches logical chunk (l%8) ^ swz_key(row).
     const int lrow = lane >> 3;
-    const int lchunk = (lane & 7) ^ lrow;
     uint32_t a_off[A_LOADS], b_off[B_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
         const int r = (wave * A_LOADS + i) * 8 + lrow;
+        const int lchunk = (lane & 7) ^ swz_key(r);
         a_off[i] = static_cast<uint32_t>((r * K + lchunk * 8) * 2);
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
         const int r = (wave * B_LOADS + i) * 8 + lrow;
+        const int lchunk = (lane & 7) ^ swz_key(r);
         int64_t brow;
         if constexpr (SWIGLU) {
             const int wcol = r / WTN, w = r % WTN;
