@@ -265,6 +265,10 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 // ---------------------------------------------------------------------------
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format
 constexpr int kFastStage = (256 + 256) * kBK;  // bf16 elements per LDS stage (A then B)
+#ifndef MOE_FAST_WAVE_COLS
+#define MOE_FAST_WAVE_COLS 4
+#endif
+constexpr int kFastWaveCols = MOE_FAST_WAVE_COLS;  // 4 -> 8 wavefronts per tile
 
 // Resource descriptor from wave-uniform values, pinned to SGPRs with readfirstlane
 // so buffer instructions take it directly (no waterfall loop).
@@ -284,20 +288,24 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint16_t* lds
         0, 0);
 }
 
-template <int SMT, bool SWIGLU>
+// WN wave columns x 2 wave rows; WN = 4 gives 8 wavefronts (2 per SIMD), each
+// owning (TM/2) x 64, so one wave's stalls are covered by the other's MFMAs.
+template <int SMT, int WN, bool SWIGLU>
 __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, int expert, int n_tile,
                                           int64_t row0, int64_t row_end) {
+    constexpr int WAVES = 2 * WN;
     constexpr int TM = SMT * 64;        // rows of this tile (2 wave rows x SMT x 32)
     constexpr int WTM = TM / 2;
-    constexpr int WTN = 128;
-    constexpr int SN = 4;
-    constexpr int A_LOADS = TM / 32;    // 8-row wavefront loads per wave
-    constexpr int B_LOADS = 8;
+    constexpr int WTN = 256 / WN;
+    constexpr int SN = WTN / 32;
+    constexpr int A_LOADS = TM / 8 / WAVES;   // 8-row wavefront loads per wave
+    constexpr int B_LOADS = 256 / 8 / WAVES;
+    static_assert(A_LOADS >= 1 && SN % 2 == 0, "tile shape");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
+    const int wm = wave / WN;
+    const int wn = wave % WN;
     const int64_t K = p.k;
 
     const int64_t a_rows = min<int64_t>(row_end - row0, TM);
@@ -449,8 +457,8 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
     }
 }
 
-template <bool SWIGLU>
-__global__ __launch_bounds__(kGemmThreads) void grouped_gemm_fast_kernel(GemmParams p) {
+template <int WN, bool SWIGLU>
+__global__ __launch_bounds__(128 * WN) void grouped_gemm_fast_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * kFastStage];
     const int32_t* __restrict__ offs = p.offsets;
     int total = 0;
@@ -475,9 +483,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_fast_kernel(GemmPar
     const int64_t row_end = min(static_cast<int64_t>(offs[expert + 1]), p.rows);
     if (row0 < 0 || row0 >= row_end) return;
     const int rem = span - m_tile * 256;  // rows left from this tile on
-    if (rem > 128) fast_tile<4, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
-    else if (rem > 64) fast_tile<2, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
-    else fast_tile<1, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
+    if (rem > 128) fast_tile<4, WN, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
+    else if (rem > 64) fast_tile<2, WN, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
+    else fast_tile<1, WN, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
 }
 
 // ---------------------------------------------------------------------------
@@ -494,8 +502,8 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     if (blocks == 0) return MOE_OK;
     if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
     if (BM == 256 && BN == 256 && p.k % kBK == 0) {
-        hipLaunchKernelGGL((grouped_gemm_fast_kernel<SWIGLU>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(kGemmThreads), 0, stream, p);
+        hipLaunchKernelGGL((grouped_gemm_fast_kernel<kFastWaveCols, SWIGLU>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(128 * kFastWaveCols), 0, stream, p);
         return check_launch("grouped_gemm_fast_kernel");
     }
     hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, SWIGLU>),
