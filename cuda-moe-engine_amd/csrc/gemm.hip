@@ -375,12 +375,16 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
             fb[j] = *reinterpret_cast<const bf16x8_t*>(&sb[swz(r, chunk)]);
         }
     };
+    // Weights fragment as src0, activations as src1: the 32x32 result comes out
+    // transposed, so lane l holds row l%32 and, in registers 4q..4q+3, the four
+    // consecutive columns 8q + 4*(l/32) + 0..3 (packed 8-byte stores). The
+    // products and their k grouping are unchanged.
     auto mma = [&](const bf16x8_t (&fa)[SMT], const bf16x8_t (&fb)[SN]) {
 #pragma unroll
         for (int i = 0; i < SMT; ++i)
 #pragma unroll
             for (int j = 0; j < SN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
     };
     // sched_barrier(0) fences keep each phase in place: the fragment reads of
     // slice kk+1 are issued before the MFMAs of slice kk, so LDS latency hides
@@ -420,37 +424,44 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
         fence();
     }
 
-    const int col_in = lane & 31;
-    const int row_in = (lane >> 5) * 4;
-    if constexpr (SWIGLU) {
+    // Epilogue: one row per lane, four consecutive columns per 8-byte store.
+    const int col4 = 4 * (lane >> 5);
 #pragma unroll
-        for (int i = 0; i < SMT; ++i) {
+    for (int i = 0; i < SMT; ++i) {
+        const int64_t grow = row0 + wm * WTM + i * 32 + (lane & 31);
+        if (grow >= row_end) continue;
+        uint16_t* crow = p.c + grow * p.ldc;
+        if constexpr (SWIGLU) {
 #pragma unroll
             for (int j = 0; j < SN / 2; ++j) {
-                const int64_t col = static_cast<int64_t>(n_tile) * 128 + wn * (WTN / 2) + j * 32 + col_in;
-                if (col >= p.n_out) continue;
+                const int64_t cbase = static_cast<int64_t>(n_tile) * 128 + wn * (WTN / 2) + j * 32 + col4;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t grow = row0 + wm * WTM + i * 32 + (r >> 2) * 8 + row_in + (r & 3);
-                    if (grow < row_end) {
-                        const float g = bf16_to_f32(f32_to_bf16(acc[i][j][r]));
-                        const float u = bf16_to_f32(f32_to_bf16(acc[i][j + SN / 2][r]));
-                        p.c[grow * p.ldc + col] = f32_to_bf16(silu_f32(g) * u);
+                for (int q = 0; q < 4; ++q) {
+                    const int64_t col = cbase + 8 * q;
+                    if (col >= p.n_out) continue;
+                    float act[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t gu = pack_bf16x2(acc[i][j][4 * q + t], acc[i][j + SN / 2][4 * q + t]);
+                        const float g = __uint_as_float(gu << 16);
+                        const float u = __uint_as_float(gu & 0xffff0000u);
+                        act[t] = silu_f32(g) * u;
                     }
+                    *reinterpret_cast<uint2*>(crow + col) =
+                        make_uint2(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]));
                 }
             }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < SMT; ++i) {
+        } else {
 #pragma unroll
             for (int j = 0; j < SN; ++j) {
-                const int64_t col = static_cast<int64_t>(n_tile) * 256 + wn * WTN + j * 32 + col_in;
-                if (col >= p.n_out) continue;
+                const int64_t cbase = static_cast<int64_t>(n_tile) * 256 + wn * WTN + j * 32 + col4;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t grow = row0 + wm * WTM + i * 32 + (r >> 2) * 8 + row_in + (r & 3);
-                    if (grow < row_end) p.c[grow * p.ldc + col] = f32_to_bf16(acc[i][j][r]);
+                for (int q = 0; q < 4; ++q) {
+                    const int64_t col = cbase + 8 * q;
+                    if (col >= p.n_out) continue;
+                    *reinterpret_cast<uint2*>(crow + col) =
+                        make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                   pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
                 }
             }
         }

@@ -21,12 +21,30 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
     return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round-to-nearest-even; NaN stays a quiet NaN with its sign.
+// Round-to-nearest-even; NaN becomes the quiet NaN (bits >> 16) | 0x40. gfx950's
+// v_cvt_pk_bf16_f32 implements exactly this mapping (checked against the
+// integer formulation on all 2^32 inputs), so conversions use the instruction.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const float2_t f = {lo, hi};
+    const bf16x2_t h = __builtin_convertvector(f, bf16x2_t);
+    uint32_t u;
+    __builtin_memcpy(&u, &h, 4);
+    return u;
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    const __bf16 h = static_cast<__bf16>(f);
+    uint16_t u;
+    __builtin_memcpy(&u, &h, 2);
+    return u;
+}
+
+// Value of f rounded to bf16, as fp32.
+__device__ __forceinline__ float round_bf16(float f) {
+    return __uint_as_float(static_cast<uint32_t>(f32_to_bf16(f)) << 16);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
