@@ -1,6 +1,6 @@
 // Routing kernels for gfx950: bias + top-k (ties to the lower expert id) +
 // selected-score softmax, on given logits or with the fp32 router projection
-// fused in.
+// fused in (on MFMA, see router_fused_kernel).
 //
 // Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:325-376 (tie rule
 // :331-333, K=2 weight formula :366-374) and src/moe_dispatch/layer.py:122-135.
@@ -103,127 +103,129 @@ __global__ __launch_bounds__(256) void topk_route_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Fused router. A block of 256 threads owns 32 tokens, 8 lanes per token.
-// The fp32 router matrix is staged through LDS in column chunks shared by the
-// 32 tokens; each lane accumulates EB partial dot products over its columns
-// (x converted exactly from bf16), then the 8 lanes of a token reduce with a
-// butterfly and lane 0 performs the top-k selection.
+// Fused router on MFMA. logits = x . W^T with x bf16 and W fp32: W is split
+// exactly-to-24-bits into three bf16 parts (hi = bf16(W), mid = bf16(W - hi),
+// lo = bf16(W - hi - mid)), so x . W = x . hi + x . mid + x . lo with exact
+// bf16 x bf16 products accumulated in fp32 by v_mfma_f32_16x16x32_bf16.
+// A block (4 wavefronts) owns 16 tokens; the waves split the hidden dimension
+// in interleaved 32-wide slices, their partial logits are added in a fixed
+// order through LDS, then each wave runs the top-k of 4 tokens with one lane
+// per expert. Reading x once is the only HBM traffic of consequence.
 // ---------------------------------------------------------------------------
-constexpr int kRouterTokens = 32;
-constexpr int kRouterLdsFloats = 8192;  // 32 KiB of router weights per chunk
+typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
+typedef float rfloatx4_t __attribute__((ext_vector_type(4)));
+constexpr int kRouterTokens = 16;
 
-template <int EB>
+__device__ __forceinline__ void split3(const float (&w)[8], rbf16x8_t& hi, rbf16x8_t& mid, rbf16x8_t& lo) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float h = round_bf16(w[j]);
+        const float r1 = w[j] - h;  // exact
+        const float m = round_bf16(r1);
+        const float r2 = r1 - m;    // exact
+        hi[j] = static_cast<__bf16>(h);
+        mid[j] = static_cast<__bf16>(m);
+        lo[j] = static_cast<__bf16>(r2);
+    }
+}
+
+template <int NT>  // expert column tiles of 16: E <= 16 * NT
 __global__ __launch_bounds__(256) void router_fused_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ router_w,
     const float* __restrict__ bias, int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
     float* __restrict__ weights, float* __restrict__ logits_out, int64_t tokens, int hidden,
     int experts, int topk) {
-    constexpr int HC = kRouterLdsFloats / EB;  // columns per chunk (multiple of 64)
-    __shared__ __attribute__((aligned(16))) float ws[EB * HC];
+    __shared__ float part[4][kRouterTokens][16 * NT];
     const int tid = threadIdx.x;
-    const int lane8 = tid & 7;
-    const int64_t token = static_cast<int64_t>(blockIdx.x) * kRouterTokens + (tid >> 3);
-    const bool live = token < tokens;
-    const uint16_t* xrow = x + (live ? token : 0) * static_cast<int64_t>(hidden);
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRouterTokens;
+    const int m = lane & 15;   // A row (token) and B column (expert within a tile)
+    const int kq = lane >> 4;  // 8-element k block within the 32-wide slice
+    const bool live = t0 + m < tokens;
+    const uint16_t* xrow = x + (live ? t0 + m : t0) * static_cast<int64_t>(hidden);
 
-    float acc[EB];
+    rfloatx4_t acc[NT];
 #pragma unroll
-    for (int e = 0; e < EB; ++e) acc[e] = 0.0f;
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int h0 = 0; h0 < hidden; h0 += HC) {
-        // Stage router_w[:, h0:h0+HC] (zero past E or H) as [EB][HC].
-        __syncthreads();
-        for (int i = tid; i < EB * HC / 4; i += 256) {
-            const int e = (i * 4) / HC;
-            const int c = (i * 4) % HC;
-            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (e < experts) {
-                const int col = h0 + c;
-                const float* src = router_w + static_cast<int64_t>(e) * hidden + col;
-                if (col + 3 < hidden) {
-                    val = *reinterpret_cast<const float4*>(src);
-                } else {
-                    if (col + 0 < hidden) val.x = src[0];
-                    if (col + 1 < hidden) val.y = src[1];
-                    if (col + 2 < hidden) val.z = src[2];
-                }
-            }
-            *reinterpret_cast<float4*>(&ws[e * HC + c]) = val;
-        }
-        __syncthreads();
-        const int width = min(HC, hidden - h0);
-        for (int c0 = lane8 * 8; c0 < width; c0 += 64) {
-            uint4 raw = make_uint4(0, 0, 0, 0);
-            if (live) raw = *reinterpret_cast<const uint4*>(xrow + h0 + c0);
-            float xv[8];
-            xv[0] = bf16_to_f32(raw.x & 0xffff);
-            xv[1] = bf16_to_f32(raw.x >> 16);
-            xv[2] = bf16_to_f32(raw.y & 0xffff);
-            xv[3] = bf16_to_f32(raw.y >> 16);
-            xv[4] = bf16_to_f32(raw.z & 0xffff);
-            xv[5] = bf16_to_f32(raw.z >> 16);
-            xv[6] = bf16_to_f32(raw.w & 0xffff);
-            xv[7] = bf16_to_f32(raw.w >> 16);
-#pragma unroll
-            for (int e = 0; e < EB; ++e) {
-                const float4 w0 = *reinterpret_cast<const float4*>(&ws[e * HC + c0]);
-                const float4 w1 = *reinterpret_cast<const float4*>(&ws[e * HC + c0 + 4]);
-                float s = acc[e];
-                s = fmaf(xv[0], w0.x, s);
-                s = fmaf(xv[1], w0.y, s);
-                s = fmaf(xv[2], w0.z, s);
-                s = fmaf(xv[3], w0.w, s);
-                s = fmaf(xv[4], w1.x, s);
-                s = fmaf(xv[5], w1.y, s);
-                s = fmaf(xv[6], w1.z, s);
-                s = fmaf(xv[7], w1.w, s);
-                acc[e] = s;
-            }
-        }
-    }
-    // Reduce the 8 partial sums of each token.
-#pragma unroll
-    for (int e = 0; e < EB; ++e) {
-        float s = acc[e];
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 4);
-        acc[e] = s;
-    }
-    if (!live || lane8 != 0) return;
-    float v[EB];
-#pragma unroll
-    for (int e = 0; e < EB; ++e) {
-        if (e < experts) {
-            if (logits_out) logits_out[token * experts + e] = acc[e];
-            v[e] = acc[e] + bias[e];
+    for (int k0 = wave * 32; k0 < hidden; k0 += 128) {
+        const int k = k0 + kq * 8;
+        const bool kin = k < hidden;  // hidden % 8 == 0: a block is all in or all out
+        rbf16x8_t a;
+        if (live && kin) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(xrow + k);
+            __builtin_memcpy(&a, &raw, 16);
         } else {
-            v[e] = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] = static_cast<__bf16>(0.0f);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int e = nt * 16 + m;
+            float w[8];
+            if (e < experts && kin) {
+                const float4 w0 = *reinterpret_cast<const float4*>(router_w + static_cast<int64_t>(e) * hidden + k);
+                const float4 w1 = *reinterpret_cast<const float4*>(router_w + static_cast<int64_t>(e) * hidden + k + 4);
+                w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
+                w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) w[j] = 0.0f;
+            }
+            rbf16x8_t hi, mid, lo;
+            split3(w, hi, mid, lo);
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, lo, acc[nt], 0, 0, 0);
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, mid, acc[nt], 0, 0, 0);
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hi, acc[nt], 0, 0, 0);
         }
     }
-    float sel_v[kMaxTopk];
-    int sel_i[kMaxTopk];
-    uint64_t taken = 0;
+    // 16x16 result: lane l holds tokens 4*(l/16) + r, expert column l%16.
 #pragma unroll
-    for (int k = 0; k < kMaxTopk; ++k) {
-        if (k < topk) {
-            float bv = -INFINITY;
-            int bi = INT_MAX;
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int e = 0; e < EB; ++e) {
-                const bool free_e = e < experts && !((taken >> e) & 1ull);
-                // Ascending scan with strict '>' keeps the lower id on ties.
-                if (free_e && (bi == INT_MAX || v[e] > bv)) {
-                    bv = v[e];
-                    bi = e;
+        for (int r = 0; r < 4; ++r) part[wave][4 * kq + r][nt * 16 + m] = acc[nt][r];
+    __syncthreads();
+
+    // Top-k: wave w handles tokens 4w..4w+3, one lane per expert.
+    for (int i = 0; i < kRouterTokens / 4; ++i) {
+        const int tl = wave * 4 + i;
+        const int64_t token = t0 + tl;
+        if (token >= tokens) break;
+        float v = -INFINITY;
+        int idx = INT_MAX;
+        if (lane < experts) {
+            const float logit = ((part[0][tl][lane] + part[1][tl][lane]) + part[2][tl][lane]) + part[3][tl][lane];
+            if (logits_out) logits_out[token * experts + lane] = logit;
+            v = logit + bias[lane];
+            idx = lane;
+        }
+        float sel_v[kMaxTopk];
+        int sel_i[kMaxTopk];
+#pragma unroll
+        for (int k = 0; k < kMaxTopk; ++k) {
+            if (k < topk) {
+                float bv = v;
+                int bi = idx;
+#pragma unroll
+                for (int msk = 32; msk >= 1; msk >>= 1) {
+                    const float ov = __shfl_xor(bv, msk);
+                    const int oi = __shfl_xor(bi, msk);
+                    if (ov > bv || (ov == bv && oi < bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                sel_v[k] = bv;
+                sel_i[k] = bi;
+                if (idx == bi) {
+                    v = -INFINITY;
+                    idx = INT_MAX;
                 }
             }
-            sel_v[k] = bv;
-            sel_i[k] = bi;
-            taken |= 1ull << bi;
         }
+        if (lane == 0) write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
     }
-    write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
 }
 
 // ---------------------------------------------------------------------------
@@ -266,18 +268,16 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
                         int64_t tokens, int hidden, int experts, int topk, hipStream_t stream) {
     if (tokens == 0) return MOE_OK;
     const dim3 grid(static_cast<unsigned>((tokens + kRouterTokens - 1) / kRouterTokens));
-#define MOE_ROUTER_CASE(EBV)                                                               \
-    hipLaunchKernelGGL(router_fused_kernel<EBV>, grid, dim3(256), 0, stream, x, router_w,  \
+#define MOE_ROUTER_CASE(NTV)                                                               \
+    hipLaunchKernelGGL(router_fused_kernel<NTV>, grid, dim3(256), 0, stream, x, router_w,  \
                        bias, ids32, ids64, weights, logits_out, tokens, hidden, experts,   \
                        topk)
-    if (experts <= 8) {
-        MOE_ROUTER_CASE(8);
-    } else if (experts <= 16) {
-        MOE_ROUTER_CASE(16);
+    if (experts <= 16) {
+        MOE_ROUTER_CASE(1);
     } else if (experts <= 32) {
-        MOE_ROUTER_CASE(32);
+        MOE_ROUTER_CASE(2);
     } else if (experts <= 64) {
-        MOE_ROUTER_CASE(64);
+        MOE_ROUTER_CASE(4);
     } else {
         return fail(MOE_ERR_UNSUPPORTED, "experts=%d exceeds 64", experts);
     }
