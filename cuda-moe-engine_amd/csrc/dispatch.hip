@@ -1,6 +1,7 @@
-// Token transport kernels for gfx950: deterministic dispatch (histogram,
-// prefix scan, stable pack with fused padding) and the atomic-free weighted
-// combine. Plus the standalone SwiGLU kept for API parity.
+// Token transport kernels for gfx950: deterministic dispatch (per-chunk
+// histogram and stable ranks, a one-block scan, then a stable pack with fused
+// padding) and the atomic-free weighted combine. Plus the standalone SwiGLU
+// kept for API parity.
 //
 // Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:13-93 (count, scan,
 // pack, combine), :194-275 (aligned layout and padding), :277-323 (SwiGLU).
@@ -13,75 +14,124 @@
 
 namespace moe {
 
-// ---------------------------------------------------------------------------
-// Stage 1: per-chunk histogram and in-chunk stable rank.
-// A chunk is `chunk_tokens` consecutive tokens (chunk_tokens*K assignments).
-// slots[p] <- rank of p among the chunk's earlier assignments to the same
-// expert; chunk_counts[c][e] <- assignments of chunk c to expert e.
-// ---------------------------------------------------------------------------
-constexpr int kRankThreads = 1024;
+// Assignments are grouped in chunks of kChunkTokens consecutive tokens.
+constexpr int kChunkTokens = 16;
+constexpr int kRankThreads = kChunkTokens * kMaxTopk;  // one thread per assignment
 constexpr int kRankWaves = kRankThreads / kWave;
 
+// ---------------------------------------------------------------------------
+// Stage 1: per-chunk histogram and in-chunk stable rank (one block per chunk).
+// slots[p] <- rank of p among the chunk's earlier assignments to the same
+// expert (-1 for an out-of-range id); chunk_counts[c][e] <- assignments of
+// chunk c to expert e.
+// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
     const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
-    int32_t* __restrict__ chunk_counts, int64_t n_assign, int experts, int64_t chunk_assign) {
-    __shared__ int running[kMaxExperts];
+    int32_t* __restrict__ chunk_counts, int64_t n_assign, int experts, int topk) {
     __shared__ int wave_counts[kRankWaves][kMaxExperts];
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid % kWave;
     const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * chunk_assign;
-    const int64_t p1 = min(p0 + chunk_assign, n_assign);
-    if (tid < kMaxExperts) running[tid] = 0;
-    for (int64_t base = p0; base < p1; base += kRankThreads) {
-        for (int i = tid; i < kRankWaves * kMaxExperts; i += kRankThreads)
-            (&wave_counts[0][0])[i] = 0;
-        __syncthreads();
-        const int64_t p = base + tid;
-        const bool valid = p < p1;
-        const int e = valid ? ids[p] : -1;
-        const bool in_range = valid && e >= 0 && e < experts;
-        // Lanes holding the same expert id: intersect 6 bit-plane ballots.
-        uint64_t same = __ballot(in_range);
+    for (int i = tid; i < kRankWaves * kMaxExperts; i += kRankThreads) (&wave_counts[0][0])[i] = 0;
+    __syncthreads();
+    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kChunkTokens * topk;
+    const int64_t p = p0 + tid;
+    const bool valid = tid < kChunkTokens * topk && p < n_assign;
+    const int e = valid ? ids[p] : -1;
+    const bool in_range = valid && e >= 0 && e < experts;
+    // Lanes holding the same expert id: intersect 6 bit-plane ballots.
+    uint64_t same = __ballot(in_range);
 #pragma unroll
-        for (int b = 0; b < 6; ++b) {
-            const bool bit = (e >> b) & 1;
-            const uint64_t plane = __ballot(in_range && bit);
-            same &= bit ? plane : ~plane;
-        }
-        const int rank = __popcll(same & lanes_below);
-        if (in_range && rank == 0) wave_counts[wave][e] = __popcll(same);
-        __syncthreads();
-        if (valid) {
-            int s = -1;
-            if (in_range) {
-                s = running[e] + rank;
-                for (int w = 0; w < wave; ++w) s += wave_counts[w][e];
-            }
-            slots[p] = s;
-        }
-        __syncthreads();
-        if (tid < experts) {
-            int add = 0;
-            for (int w = 0; w < kRankWaves; ++w) add += wave_counts[w][tid];
-            running[tid] += add;
-        }
-        __syncthreads();
+    for (int b = 0; b < 6; ++b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t plane = __ballot(in_range && bit);
+        same &= bit ? plane : ~plane;
     }
-    if (tid < experts) chunk_counts[static_cast<int64_t>(blockIdx.x) * experts + tid] = running[tid];
+    const int rank = __popcll(same & lanes_below);
+    if (in_range && rank == 0) wave_counts[wave][e] = __popcll(same);
+    __syncthreads();
+    if (valid) {
+        int s = -1;
+        if (in_range) {
+            s = rank;
+            for (int w = 0; w < wave; ++w) s += wave_counts[w][e];
+        }
+        slots[p] = s;
+    }
+    if (tid < experts) {
+        int total = 0;
+        for (int w = 0; w < kRankWaves; ++w) total += wave_counts[w][tid];
+        chunk_counts[static_cast<int64_t>(blockIdx.x) * experts + tid] = total;
+    }
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2: prefix + pack + padding. A block owns `pack_tokens` tokens of one
-// chunk. It rebuilds, from chunk_counts, the expert totals (-> counts and
-// aligned offsets, written by block 0) and the counts of earlier chunks, turns
-// in-chunk ranks into within-expert slots and destinations, and copies each
-// token row once from x to its K destinations with VB-byte accesses. Blocks
-// e, e+grid, ... also zero the padding rows of expert e.
+// Stage 2 (one block): chunk_counts[c][e] -> exclusive prefix over chunks
+// (in place, the chunk's base slot for expert e), counts[e] = totals,
+// offsets[e+1] = offsets[e] + ceil(counts[e]/a)*a. 16 groups of 64 threads
+// each own a contiguous run of chunks; thread (g, e) walks its run twice.
+// ---------------------------------------------------------------------------
+constexpr int kScanGroups = 16;
+
+__global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
+    int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int n_chunks, int experts, int alignment) {
+    __shared__ int seg_sum[kScanGroups][kMaxExperts];
+    __shared__ int seg_base[kScanGroups][kMaxExperts];
+    const int tid = threadIdx.x;
+    const int e = tid % kMaxExperts;
+    const int g = tid / kMaxExperts;
+    const int per = (n_chunks + kScanGroups - 1) / kScanGroups;
+    const int c0 = g * per;
+    const int c1 = min(n_chunks, c0 + per);
+    int sum = 0;
+    if (e < experts)
+        for (int c = c0; c < c1; ++c) sum += chunk_counts[static_cast<int64_t>(c) * experts + e];
+    seg_sum[g][e] = sum;
+    __syncthreads();
+    if (tid < kMaxExperts) {
+        int running = 0;
+        for (int gg = 0; gg < kScanGroups; ++gg) {
+            seg_base[gg][tid] = running;
+            running += seg_sum[gg][tid];
+        }
+        // Wave 0: totals, aligned spans and their inclusive scan over experts.
+        const int total = tid < experts ? running : 0;
+        const int span = (total + alignment - 1) / alignment * alignment;
+        int incl = span;
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int up = __shfl_up(incl, d);
+            if (tid >= d) incl += up;
+        }
+        if (tid < experts) {
+            counts[tid] = total;
+            offsets[tid + 1] = incl;
+        }
+        if (tid == 0) offsets[0] = 0;
+    }
+    __syncthreads();
+    if (e < experts) {
+        int running = seg_base[g][e];
+        for (int c = c0; c < c1; ++c) {
+            const int64_t at = static_cast<int64_t>(c) * experts + e;
+            const int v = chunk_counts[at];
+            chunk_counts[at] = running;
+            running += v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 3: pack. A block owns `pack_tokens` tokens of one chunk: slot = chunk
+// base + in-chunk rank, dest = offsets[e] + slot (inverse and slots written),
+// then each x row is read once and written to its K destinations with VB-byte
+// accesses, kLoads accesses in flight per thread. Blocks e, e+grid, ... zero
+// the padding rows of expert e.
 // ---------------------------------------------------------------------------
 constexpr int kPackThreads = 256;
-constexpr int kPackMaxAssign = 256;  // pack_tokens * K upper bound
+constexpr int kPackMaxAssign = 128;  // pack_tokens * K upper bound
+constexpr int kPackLoads = 4;        // vectors per thread per pass
 
 template <int VB> struct VecOf;
 template <> struct VecOf<16> { using T = uint4; };
@@ -98,122 +148,78 @@ template <> __device__ __forceinline__ uint16_t zero_vec<uint16_t>() { return 0;
 template <int VB>
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
-    const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
-    int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
-    int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
-    int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2) {
+    const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
+    int64_t tokens, int64_t row_bytes, int experts, int topk, int pack_tokens) {
     using V = typename VecOf<VB>::T;
-    __shared__ int part_all[kPackThreads / kWave][kMaxExperts];
-    __shared__ int part_before[kPackThreads / kWave][kMaxExperts];
-    __shared__ int total[kMaxExperts];
-    __shared__ int before[kMaxExperts];
-    __shared__ int offs[kMaxExperts + 1];
     __shared__ int64_t dest[kPackMaxAssign];
-
     const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid % kWave;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * pack_tokens;
-    const int my_chunk = static_cast<int>(t0 / chunk_tokens);
-
-    // (a) Column sums of chunk_counts: all chunks, and chunks before mine.
-    //     Thread tid always sees expert tid % experts_pow2 (a divisor of 256).
-    {
-        const int e = tid % experts_pow2;
-        int s_all = 0, s_before = 0;
-        if (e < experts) {
-            for (int c = tid / experts_pow2; c < n_chunks; c += kPackThreads / experts_pow2) {
-                const int v = chunk_counts[static_cast<int64_t>(c) * experts + e];
-                s_all += v;
-                if (c < my_chunk) s_before += v;
-            }
-        }
-        for (int m = experts_pow2; m < kWave; m <<= 1) {
-            s_all += __shfl_xor(s_all, m);
-            s_before += __shfl_xor(s_before, m);
-        }
-        if (lane < experts_pow2 && lane < kMaxExperts) {
-            part_all[wave][lane] = s_all;
-            part_before[wave][lane] = s_before;
-        }
-    }
-    __syncthreads();
-    if (wave == 0) {
-        int tot = 0, bef = 0;
-        if (lane < experts) {
-            for (int w = 0; w < kPackThreads / kWave; ++w) {
-                tot += part_all[w][lane];
-                bef += part_before[w][lane];
-            }
-        }
-        const int span = (tot + alignment - 1) / alignment * alignment;
-        int incl = span;  // inclusive scan over the wavefront
-        for (int d = 1; d < kWave; d <<= 1) {
-            const int up = __shfl_up(incl, d);
-            if (lane >= d) incl += up;
-        }
-        if (lane < experts) {
-            total[lane] = tot;
-            before[lane] = bef;
-            offs[lane + 1] = incl;
-        }
-        if (lane == 0) offs[0] = 0;
-    }
-    __syncthreads();
-    if (blockIdx.x == 0) {
-        if (tid < experts) counts[tid] = total[tid];
-        if (tid <= experts) offsets[tid] = offs[tid];
-    }
-
-    // (b) Destinations of this block's assignments.
+    const int64_t chunk = t0 / kChunkTokens;
     const int64_t t_end = min(t0 + pack_tokens, tokens);
     const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
     const int n_local = n_tok * topk;
     for (int i = tid; i < n_local; i += kPackThreads) {
-        const int64_t p = t0 * topk + i;
-        const int e = ids[p];
+        const int64_t pa = t0 * topk + i;
+        const int e = ids[pa];
         int64_t d = -1;
         if (e >= 0 && e < experts) {
-            const int r = slots[p];
+            const int r = slots[pa];
             if (r >= 0) {
-                const int slot = before[e] + r;
-                d = static_cast<int64_t>(offs[e]) + slot;
-                slots[p] = slot;
-                inverse[p] = static_cast<int32_t>(d);
+                const int slot = chunk_base[chunk * experts + e] + r;
+                d = static_cast<int64_t>(offsets[e]) + slot;
+                slots[pa] = slot;
+                inverse[pa] = static_cast<int32_t>(d);
             }
         }
         dest[i] = d;
     }
     __syncthreads();
 
-    // (c) Row copies: each x row is read once and written to its K rows.
     const int64_t nv = row_bytes / VB;
     const int64_t items = static_cast<int64_t>(n_tok) * nv;
-    for (int64_t i = tid; i < items; i += kPackThreads) {
-        const int tl = static_cast<int>(i / nv);
-        const int64_t v = i - static_cast<int64_t>(tl) * nv;
-        const V val = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[v];
-        for (int k = 0; k < topk; ++k) {
-            const int64_t d = dest[tl * topk + k];
-            if (d >= 0) reinterpret_cast<V*>(packed + d * row_bytes)[v] = val;
+    for (int64_t base = 0; base < items; base += static_cast<int64_t>(kPackThreads) * kPackLoads) {
+        V val[kPackLoads];
+#pragma unroll
+        for (int u = 0; u < kPackLoads; ++u) {
+            const int64_t i = base + tid + u * kPackThreads;
+            if (i < items) {
+                const int64_t tl = i / nv;
+                val[u] = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[i - tl * nv];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kPackLoads; ++u) {
+            const int64_t i = base + tid + u * kPackThreads;
+            if (i < items) {
+                const int tl = static_cast<int>(i / nv);
+                const int64_t v = i - static_cast<int64_t>(tl) * nv;
+                for (int k = 0; k < topk; ++k) {
+                    const int64_t d = dest[tl * topk + k];
+                    if (d >= 0) reinterpret_cast<V*>(packed + d * row_bytes)[v] = val[u];
+                }
+            }
         }
     }
 
-    // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
+    // Padding rows [offsets[e] + counts[e], offsets[e+1]) are zero.
     for (int e = blockIdx.x; e < experts; e += gridDim.x) {
-        const int64_t r0 = offs[e] + total[e];
-        const int64_t r1 = offs[e + 1];
+        const int64_t r0 = static_cast<int64_t>(offsets[e]) + counts[e];
+        const int64_t r1 = offsets[e + 1];
         const int64_t pad_items = (r1 - r0) * nv;
-        V* base = reinterpret_cast<V*>(packed + r0 * row_bytes);
-        for (int64_t i = tid; i < pad_items; i += kPackThreads) base[i] = zero_vec<V>();
+        V* out = reinterpret_cast<V*>(packed + r0 * row_bytes);
+        for (int64_t i = tid; i < pad_items; i += kPackThreads) out[i] = zero_vec<V>();
     }
 }
 
 // ---------------------------------------------------------------------------
 // Combine: out[t] = round(sum_k w[t,k] * y[inverse[t,k]]) in fp32, k order,
 // separate multiply and add (no contraction), skipped rows outside [0, R).
-// One thread per (token, VE-element vector).
+// Each thread owns kCombineVecs VE-element vectors of one token and issues
+// all K * kCombineVecs gathers before reducing.
 // ---------------------------------------------------------------------------
+constexpr int kCombineVecs = 2;
+
 template <int DT, int VE>
 __global__ __launch_bounds__(256) void combine_kernel(
     const typename Elem<DT>::T* __restrict__ y, const int32_t* __restrict__ inverse,
@@ -225,30 +231,58 @@ __global__ __launch_bounds__(256) void combine_kernel(
         T v[VE];
     };
     const int64_t nv = hidden / VE;
+    const int64_t groups = (nv + kCombineVecs - 1) / kCombineVecs;  // vector groups per token
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t t = idx / nv;
+    const int64_t t = idx / groups;
     if (t >= tokens) return;
-    const int64_t v = idx - t * nv;
-    float acc[VE];
+    const int64_t v0 = (idx - t * groups) * kCombineVecs;
+    float acc[kCombineVecs][VE];
 #pragma unroll
-    for (int j = 0; j < VE; ++j) acc[j] = 0.0f;
-    for (int k = 0; k < topk; ++k) {
-        const int64_t p = t * topk + k;
-        const int row = inverse[p];
-        if (row >= 0 && row < rows) {
-            const float w = weights[p];
-            const Pack in = reinterpret_cast<const Pack*>(y + static_cast<int64_t>(row) * hidden)[v];
+    for (int u = 0; u < kCombineVecs; ++u)
 #pragma unroll
-            for (int j = 0; j < VE; ++j) {
-                const float prod = w * Elem<DT>::load(in.v[j]);
-                acc[j] = acc[j] + prod;
+        for (int j = 0; j < VE; ++j) acc[u][j] = 0.0f;
+    for (int k0 = 0; k0 < topk; k0 += 2) {
+        Pack in[2][kCombineVecs];
+        float w[2];
+        bool ok[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int k = k0 + kk;
+            ok[kk] = false;
+            w[kk] = 0.0f;
+            if (k < topk) {
+                const int64_t pa = t * topk + k;
+                const int row = inverse[pa];
+                ok[kk] = row >= 0 && row < rows;
+                if (ok[kk]) {
+                    w[kk] = weights[pa];
+                    const Pack* src = reinterpret_cast<const Pack*>(y + static_cast<int64_t>(row) * hidden);
+#pragma unroll
+                    for (int u = 0; u < kCombineVecs; ++u)
+                        if (v0 + u < nv) in[kk][u] = src[v0 + u];
+                }
             }
         }
-    }
-    Pack o;
 #pragma unroll
-    for (int j = 0; j < VE; ++j) o.v[j] = Elem<DT>::store(acc[j]);
-    reinterpret_cast<Pack*>(out + t * hidden)[v] = o;
+        for (int kk = 0; kk < 2; ++kk) {
+            if (!ok[kk]) continue;
+#pragma unroll
+            for (int u = 0; u < kCombineVecs; ++u)
+#pragma unroll
+                for (int j = 0; j < VE; ++j) {
+                    const float prod = w[kk] * Elem<DT>::load(in[kk][u].v[j]);
+                    acc[u][j] = acc[u][j] + prod;
+                }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kCombineVecs; ++u) {
+        if (v0 + u >= nv) continue;
+        Pack o;
+#pragma unroll
+        for (int j = 0; j < VE; ++j) o.v[j] = Elem<DT>::store(acc[u][j]);
+        reinterpret_cast<Pack*>(out + t * hidden)[v0 + u] = o;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -279,39 +313,20 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const typename Elem<DT>::T*
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-struct DispatchPlan {
-    int64_t chunk_tokens;
-    int64_t n_chunks;
-    int pack_tokens;
-    int64_t pack_blocks;
-};
-
-static int64_t pow2_at_least(int64_t v) {
-    int64_t p = 1;
-    while (p < v) p <<= 1;
-    return p;
-}
-
-// Chunk size keeps n_chunks * E <= 1024 (each pack block rebuilds its prefix
-// from the whole chunk_counts table); pack blocks move about 16 KiB of rows.
-DispatchPlan plan_dispatch(int64_t tokens, int64_t experts, int64_t topk, int64_t row_bytes) {
-    DispatchPlan p{};
-    int64_t chunk = 16;
-    while (chunk < tokens && ((tokens + chunk - 1) / chunk) * experts > 1024) chunk <<= 1;
-    p.chunk_tokens = chunk;
-    p.n_chunks = tokens > 0 ? (tokens + chunk - 1) / chunk : 0;
-    int64_t pt = 1;
-    const int64_t max_pt = kPackMaxAssign / topk;
-    while (pt * 2 <= max_pt && pt * 2 <= chunk && pt * row_bytes < 16384) pt <<= 1;
-    p.pack_tokens = static_cast<int>(pt);
-    p.pack_blocks = tokens > 0 ? (tokens + pt - 1) / pt : 1;
-    return p;
-}
+static int64_t n_chunks_of(int64_t tokens) { return (tokens + kChunkTokens - 1) / kChunkTokens; }
 
 int64_t dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
-    const DispatchPlan p = plan_dispatch(tokens, experts, topk, 16);
-    const int64_t n = p.n_chunks * experts;
+    (void)topk;
+    const int64_t n = n_chunks_of(tokens) * experts;
     return (n > 0 ? n : 1) * static_cast<int64_t>(sizeof(int32_t));
+}
+
+// Tokens per pack block: a power of two dividing kChunkTokens, moving about
+// 32 KiB of rows per block.
+static int pack_tokens_for(int64_t row_bytes, int topk) {
+    int pt = 1;
+    while (pt * 2 <= kChunkTokens && pt * 2 * topk <= kPackMaxAssign && pt * row_bytes < 32768) pt <<= 1;
+    return pt;
 }
 
 int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts,
@@ -320,29 +335,31 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
                     int alignment, bool vectorized, hipStream_t stream) {
     const int64_t elem = dtype_size(dtype);
     const int64_t row_bytes = hidden * elem;
-    const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes);
+    const int64_t n_chunks = n_chunks_of(tokens);
     const int64_t n_assign = tokens * topk;
-    if (plan.n_chunks > 0) {
-        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)),
-                           dim3(kRankThreads), 0, stream, ids, slots, chunk_counts, n_assign,
-                           experts, plan.chunk_tokens * topk);
-        int rc = check_launch("count_rank_kernel");
+    if (n_chunks > 0) {
+        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(n_chunks)), dim3(kRankThreads),
+                           0, stream, ids, slots, chunk_counts, n_assign, experts, topk);
+        const int rc = check_launch("count_rank_kernel");
         if (rc != MOE_OK) return rc;
     }
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanGroups * kMaxExperts), 0, stream, chunk_counts,
+                       counts, offsets, static_cast<int>(n_chunks), experts, alignment);
+    int rc = check_launch("scan_kernel");
+    if (rc != MOE_OK) return rc;
     int vb = static_cast<int>(elem);
     if (vectorized) {
         if (row_bytes % 16 == 0) vb = 16;
         else if (row_bytes % 8 == 0) vb = 8;
         else if (row_bytes % 4 == 0) vb = 4;
     }
-    const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
-    const dim3 grid(static_cast<unsigned>(plan.pack_blocks));
-#define MOE_PACK_CASE(VBV)                                                                   \
-    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                \
+    const int pt = pack_tokens_for(row_bytes, topk);
+    const int64_t blocks = tokens > 0 ? (tokens + pt - 1) / pt : 1;
+    const dim3 grid(static_cast<unsigned>(std::max<int64_t>(blocks, std::min<int64_t>(experts, 64))));
+#define MOE_PACK_CASE(VBV)                                                                     \
+    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                  \
                        static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets, \
-                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,  \
-                       alignment, plan.chunk_tokens, plan.pack_tokens,                        \
-                       static_cast<int>(plan.n_chunks), experts_pow2)
+                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk, pt)
     switch (vb) {
         case 16: MOE_PACK_CASE(16); break;
         case 8: MOE_PACK_CASE(8); break;
@@ -359,7 +376,8 @@ static void launch_combine_t(const void* y, const int32_t* inverse, const float*
                              void* out, int64_t tokens, int64_t hidden, int topk, int64_t rows,
                              hipStream_t stream) {
     using T = typename Elem<DT>::T;
-    const int64_t threads = tokens * (hidden / VE);
+    const int64_t groups = (hidden / VE + kCombineVecs - 1) / kCombineVecs;
+    const int64_t threads = tokens * groups;
     const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
     hipLaunchKernelGGL((combine_kernel<DT, VE>), grid, dim3(256), 0, stream,
                        static_cast<const T*>(y), inverse, weights, static_cast<T*>(out), tokens,

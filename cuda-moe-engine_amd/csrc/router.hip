@@ -149,35 +149,48 @@ __global__ __launch_bounds__(256) void router_fused_kernel(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int k0 = wave * 32; k0 < hidden; k0 += 128) {
-        const int k = k0 + kq * 8;
-        const bool kin = k < hidden;  // hidden % 8 == 0: a block is all in or all out
-        rbf16x8_t a;
-        if (live && kin) {
-            const uint4 raw = *reinterpret_cast<const uint4*>(xrow + k);
-            __builtin_memcpy(&a, &raw, 16);
-        } else {
+    // Slices are visited in batches of kBatch with every load of a batch issued
+    // before its MFMAs, so each wave keeps several 16-byte loads in flight.
+    constexpr int kBatch = 8;
+    for (int kb = wave * 32; kb < hidden; kb += 128 * kBatch) {
+        rbf16x8_t a[kBatch];
+        float w[kBatch][NT][8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a[j] = static_cast<__bf16>(0.0f);
-        }
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int e = nt * 16 + m;
-            float w[8];
-            if (e < experts && kin) {
-                const float4 w0 = *reinterpret_cast<const float4*>(router_w + static_cast<int64_t>(e) * hidden + k);
-                const float4 w1 = *reinterpret_cast<const float4*>(router_w + static_cast<int64_t>(e) * hidden + k + 4);
-                w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
-                w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
+        for (int u = 0; u < kBatch; ++u) {
+            const int k = kb + u * 128 + kq * 8;
+            const bool kin = k < hidden;  // hidden % 8 == 0: a block is all in or all out
+            if (live && kin) {
+                const uint4 raw = *reinterpret_cast<const uint4*>(xrow + k);
+                __builtin_memcpy(&a[u], &raw, 16);
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) w[j] = 0.0f;
+                for (int j = 0; j < 8; ++j) a[u][j] = static_cast<__bf16>(0.0f);
             }
-            rbf16x8_t hi, mid, lo;
-            split3(w, hi, mid, lo);
-            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, lo, acc[nt], 0, 0, 0);
-            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, mid, acc[nt], 0, 0, 0);
-            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hi, acc[nt], 0, 0, 0);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int e = nt * 16 + m;
+                if (e < experts && kin) {
+                    const float* src = router_w + static_cast<int64_t>(e) * hidden + k;
+                    const float4 w0 = *reinterpret_cast<const float4*>(src);
+                    const float4 w1 = *reinterpret_cast<const float4*>(src + 4);
+                    w[u][nt][0] = w0.x; w[u][nt][1] = w0.y; w[u][nt][2] = w0.z; w[u][nt][3] = w0.w;
+                    w[u][nt][4] = w1.x; w[u][nt][5] = w1.y; w[u][nt][6] = w1.z; w[u][nt][7] = w1.w;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) w[u][nt][j] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                rbf16x8_t hi, mid, lo;
+                split3(w[u][nt], hi, mid, lo);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], lo, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], mid, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], hi, acc[nt], 0, 0, 0);
+            }
         }
     }
     // 16x16 result: lane l holds tokens 4*(l/16) + r, expert column l%16.
