@@ -73,6 +73,7 @@ __global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
 // each own a contiguous run of chunks; thread (g, e) walks its run twice.
 // ---------------------------------------------------------------------------
 constexpr int kScanGroups = 16;
+constexpr int kScanBatch = 16;
 
 __global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
     int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
@@ -85,9 +86,18 @@ __global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
     const int per = (n_chunks + kScanGroups - 1) / kScanGroups;
     const int c0 = g * per;
     const int c1 = min(n_chunks, c0 + per);
+    // Loads are issued in batches of kScanBatch so each walk is not latency bound.
     int sum = 0;
-    if (e < experts)
-        for (int c = c0; c < c1; ++c) sum += chunk_counts[static_cast<int64_t>(c) * experts + e];
+    if (e < experts) {
+        for (int cb = c0; cb < c1; cb += kScanBatch) {
+            int v[kScanBatch];
+#pragma unroll
+            for (int u = 0; u < kScanBatch; ++u)
+                v[u] = (cb + u < c1) ? chunk_counts[static_cast<int64_t>(cb + u) * experts + e] : 0;
+#pragma unroll
+            for (int u = 0; u < kScanBatch; ++u) sum += v[u];
+        }
+    }
     seg_sum[g][e] = sum;
     __syncthreads();
     if (tid < kMaxExperts) {
@@ -113,11 +123,16 @@ __global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
     __syncthreads();
     if (e < experts) {
         int running = seg_base[g][e];
-        for (int c = c0; c < c1; ++c) {
-            const int64_t at = static_cast<int64_t>(c) * experts + e;
-            const int v = chunk_counts[at];
-            chunk_counts[at] = running;
-            running += v;
+        for (int cb = c0; cb < c1; cb += kScanBatch) {
+            int v[kScanBatch];
+#pragma unroll
+            for (int u = 0; u < kScanBatch; ++u)
+                v[u] = (cb + u < c1) ? chunk_counts[static_cast<int64_t>(cb + u) * experts + e] : 0;
+#pragma unroll
+            for (int u = 0; u < kScanBatch; ++u) {
+                if (cb + u < c1) chunk_counts[static_cast<int64_t>(cb + u) * experts + e] = running;
+                running += v[u];
+            }
         }
     }
 }
@@ -176,27 +191,26 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     }
     __syncthreads();
 
+    // Row copies, token by token: each thread loads up to kPackLoads vectors of a
+    // row (256 apart) before storing them to the row's K destinations.
     const int64_t nv = row_bytes / VB;
-    const int64_t items = static_cast<int64_t>(n_tok) * nv;
-    for (int64_t base = 0; base < items; base += static_cast<int64_t>(kPackThreads) * kPackLoads) {
-        V val[kPackLoads];
+    for (int tl = 0; tl < n_tok; ++tl) {
+        const V* src = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes);
+        for (int64_t vb = 0; vb < nv; vb += static_cast<int64_t>(kPackThreads) * kPackLoads) {
+            V val[kPackLoads];
 #pragma unroll
-        for (int u = 0; u < kPackLoads; ++u) {
-            const int64_t i = base + tid + u * kPackThreads;
-            if (i < items) {
-                const int64_t tl = i / nv;
-                val[u] = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[i - tl * nv];
+            for (int u = 0; u < kPackLoads; ++u) {
+                const int64_t v = vb + tid + u * kPackThreads;
+                if (v < nv) val[u] = src[v];
             }
-        }
+            for (int k = 0; k < topk; ++k) {
+                const int64_t d = dest[tl * topk + k];
+                if (d < 0) continue;
+                V* dst = reinterpret_cast<V*>(packed + d * row_bytes);
 #pragma unroll
-        for (int u = 0; u < kPackLoads; ++u) {
-            const int64_t i = base + tid + u * kPackThreads;
-            if (i < items) {
-                const int tl = static_cast<int>(i / nv);
-                const int64_t v = i - static_cast<int64_t>(tl) * nv;
-                for (int k = 0; k < topk; ++k) {
-                    const int64_t d = dest[tl * topk + k];
-                    if (d >= 0) reinterpret_cast<V*>(packed + d * row_bytes)[v] = val[u];
+                for (int u = 0; u < kPackLoads; ++u) {
+                    const int64_t v = vb + tid + u * kPackThreads;
+                    if (v < nv) dst[v] = val[u];
                 }
             }
         }
@@ -321,11 +335,11 @@ int64_t dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
     return (n > 0 ? n : 1) * static_cast<int64_t>(sizeof(int32_t));
 }
 
-// Tokens per pack block: a power of two dividing kChunkTokens, moving about
-// 32 KiB of rows per block.
+// Tokens per pack block: the smallest power of two (dividing kChunkTokens)
+// whose rows reach 8 KiB, so many small blocks stay resident per CU.
 static int pack_tokens_for(int64_t row_bytes, int topk) {
     int pt = 1;
-    while (pt * 2 <= kChunkTokens && pt * 2 * topk <= kPackMaxAssign && pt * row_bytes < 32768) pt <<= 1;
+    while (pt * 2 <= kChunkTokens && pt * 2 * topk <= kPackMaxAssign && pt * row_bytes < 8192) pt <<= 1;
     return pt;
 }
 
