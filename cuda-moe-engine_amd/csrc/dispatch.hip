@@ -73,7 +73,7 @@ __global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
 // each own a contiguous run of chunks; thread (g, e) walks its run twice.
 // ---------------------------------------------------------------------------
 constexpr int kScanGroups = 16;
-constexpr int kScanBatch = 16;
+constexpr int kScanBatch = 32;
 
 __global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
     int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
@@ -86,10 +86,17 @@ __global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
     const int per = (n_chunks + kScanGroups - 1) / kScanGroups;
     const int c0 = g * per;
     const int c1 = min(n_chunks, c0 + per);
-    // Loads are issued in batches of kScanBatch so each walk is not latency bound.
+    // Loads are issued in batches of kScanBatch so each walk is not latency
+    // bound; the first batch stays in registers for the write-back phase.
     int sum = 0;
+    int first[kScanBatch];
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u)
+        first[u] = (e < experts && c0 + u < c1) ? chunk_counts[static_cast<int64_t>(c0 + u) * experts + e] : 0;
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) sum += first[u];
     if (e < experts) {
-        for (int cb = c0; cb < c1; cb += kScanBatch) {
+        for (int cb = c0 + kScanBatch; cb < c1; cb += kScanBatch) {
             int v[kScanBatch];
 #pragma unroll
             for (int u = 0; u < kScanBatch; ++u)
@@ -123,7 +130,12 @@ __global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
     __syncthreads();
     if (e < experts) {
         int running = seg_base[g][e];
-        for (int cb = c0; cb < c1; cb += kScanBatch) {
+#pragma unroll
+        for (int u = 0; u < kScanBatch; ++u) {
+            if (c0 + u < c1) chunk_counts[static_cast<int64_t>(c0 + u) * experts + e] = running;
+            running += first[u];
+        }
+        for (int cb = c0 + kScanBatch; cb < c1; cb += kScanBatch) {
             int v[kScanBatch];
 #pragma unroll
             for (int u = 0; u < kScanBatch; ++u)
@@ -174,6 +186,18 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int64_t t_end = min(t0 + pack_tokens, tokens);
     const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
     const int n_local = n_tok * topk;
+    const int64_t nv = row_bytes / VB;
+    // The first token's row loads do not depend on the destinations: issue them
+    // before the ids -> slots -> chunk base -> offsets chain.
+    V head[kPackLoads];
+    if (n_tok > 0) {
+        const V* src = reinterpret_cast<const V*>(x + t0 * row_bytes);
+#pragma unroll
+        for (int u = 0; u < kPackLoads; ++u) {
+            const int64_t v = tid + u * kPackThreads;
+            if (v < nv) head[u] = src[v];
+        }
+    }
     for (int i = tid; i < n_local; i += kPackThreads) {
         const int64_t pa = t0 * topk + i;
         const int e = ids[pa];
@@ -193,15 +217,19 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
 
     // Row copies, token by token: each thread loads up to kPackLoads vectors of a
     // row (256 apart) before storing them to the row's K destinations.
-    const int64_t nv = row_bytes / VB;
     for (int tl = 0; tl < n_tok; ++tl) {
         const V* src = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes);
         for (int64_t vb = 0; vb < nv; vb += static_cast<int64_t>(kPackThreads) * kPackLoads) {
             V val[kPackLoads];
+            if (tl == 0 && vb == 0) {
 #pragma unroll
-            for (int u = 0; u < kPackLoads; ++u) {
-                const int64_t v = vb + tid + u * kPackThreads;
-                if (v < nv) val[u] = src[v];
+                for (int u = 0; u < kPackLoads; ++u) val[u] = head[u];
+            } else {
+#pragma unroll
+                for (int u = 0; u < kPackLoads; ++u) {
+                    const int64_t v = vb + tid + u * kPackThreads;
+                    if (v < nv) val[u] = src[v];
+                }
             }
             for (int k = 0; k < topk; ++k) {
                 const int64_t d = dest[tl * topk + k];

@@ -44,6 +44,7 @@ struct GemmParams {
     int64_t rows;             // rows of A and C; spans are clamped to it
     int experts;
     int n_tiles;              // output column tiles
+    int n_cu;                 // compute units of the device (tail balancing)
 };
 
 // 16-byte chunk c of LDS row r lives at physical chunk c ^ f(r), f(r) = (r ^ (r >> 3)) & 7.
@@ -290,17 +291,20 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint16_t* lds
 
 // WN wave columns x 2 wave rows; WN = 4 gives 8 wavefronts (2 per SIMD), each
 // owning (TM/2) x 64, so one wave's stalls are covered by the other's MFMAs.
-template <int SMT, int WN, bool SWIGLU>
-__device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, int expert, int n_tile,
+// BNT weight rows per tile (256, or 128 for the split tail pieces); col0 is the
+// first output column of the tile.
+template <int SMT, int WN, int BNT, bool SWIGLU>
+__device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end) {
     constexpr int WAVES = 2 * WN;
     constexpr int TM = SMT * 64;        // rows of this tile (2 wave rows x SMT x 32)
     constexpr int WTM = TM / 2;
-    constexpr int WTN = 256 / WN;
+    constexpr int WTN = BNT / WN;
     constexpr int SN = WTN / 32;
     constexpr int A_LOADS = TM / 8 / WAVES;   // 8-row wavefront loads per wave
-    constexpr int B_LOADS = 256 / 8 / WAVES;
-    static_assert(A_LOADS >= 1 && SN % 2 == 0, "tile shape");
+    constexpr int B_LOADS = BNT / 8 / WAVES;
+    static_assert(A_LOADS >= 1 && B_LOADS >= 1 && SN >= 1, "tile shape");
+    static_assert(!SWIGLU || SN % 2 == 0, "gate/up pairing needs an even sub-tile count");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -331,10 +335,10 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
         if constexpr (SWIGLU) {
             const int wcol = r / WTN, w = r % WTN;
             constexpr int HALF = WTN / 2;
-            const int64_t col = static_cast<int64_t>(n_tile) * 128 + wcol * HALF + (w % HALF);
+            const int64_t col = col0 + wcol * HALF + (w % HALF);
             brow = (w < HALF) ? col : p.n_out + col;
         } else {
-            brow = static_cast<int64_t>(n_tile) * 256 + r;
+            brow = col0 + r;
         }
         b_off[i] = static_cast<uint32_t>((brow * K + lchunk * 8) * 2);
     }
@@ -434,7 +438,7 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
         if constexpr (SWIGLU) {
 #pragma unroll
             for (int j = 0; j < SN / 2; ++j) {
-                const int64_t cbase = static_cast<int64_t>(n_tile) * 128 + wn * (WTN / 2) + j * 32 + col4;
+                const int64_t cbase = col0 + wn * (WTN / 2) + j * 32 + col4;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int64_t col = cbase + 8 * q;
@@ -454,7 +458,7 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
         } else {
 #pragma unroll
             for (int j = 0; j < SN; ++j) {
-                const int64_t cbase = static_cast<int64_t>(n_tile) * 256 + wn * WTN + j * 32 + col4;
+                const int64_t cbase = col0 + wn * WTN + j * 32 + col4;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int64_t col = cbase + 8 * q;
@@ -468,17 +472,30 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
     }
 }
 
+// Work list: full tiles in XCD-aware order, then (plain GEMM only) the tail.
+// When the last round of full tiles would occupy at most half of the CUs,
+// those tiles are split into two 128-column pieces each; every piece still
+// runs the whole k chain in order, so results are unchanged.
 template <int WN, bool SWIGLU>
 __global__ __launch_bounds__(128 * WN) void grouped_gemm_fast_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * kFastStage];
     const int32_t* __restrict__ offs = p.offsets;
     int total = 0;
     for (int e = 0; e < p.experts; ++e) total += ((offs[e + 1] - offs[e] + 255) / 256) * p.n_tiles;
-    const int per_xcd = (total + kNumXcd - 1) / kNumXcd;
-    const int slot = blockIdx.x / kNumXcd;
-    if (slot >= per_xcd) return;
-    const int tile = (blockIdx.x % kNumXcd) * per_xcd + slot;
-    if (tile >= total) return;
+    const int rem = p.n_cu > 0 ? total % p.n_cu : 0;
+    const bool split = !SWIGLU && rem > 0 && 2 * rem <= p.n_cu;
+    const int main_tiles = split ? total - rem : total;
+    const int per_xcd = (main_tiles + kNumXcd - 1) / kNumXcd;
+    int tile, piece = -1;
+    if (static_cast<int>(blockIdx.x) < kNumXcd * per_xcd) {
+        tile = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+        if (tile >= main_tiles) return;
+    } else {
+        const int q = blockIdx.x - kNumXcd * per_xcd;
+        if (!split || q >= 2 * rem) return;
+        tile = main_tiles + q / 2;
+        piece = q % 2;
+    }
     int expert = 0, base = 0, m_tiles = 0, span = 0;
     for (; expert < p.experts; ++expert) {
         span = offs[expert + 1] - offs[expert];
@@ -493,15 +510,42 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_fast_kernel(GemmParams 
     const int64_t row0 = offs[expert] + static_cast<int64_t>(m_tile) * 256;
     const int64_t row_end = min(static_cast<int64_t>(offs[expert + 1]), p.rows);
     if (row0 < 0 || row0 >= row_end) return;
-    const int rem = span - m_tile * 256;  // rows left from this tile on
-    if (rem > 128) fast_tile<4, WN, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
-    else if (rem > 64) fast_tile<2, WN, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
-    else fast_tile<1, WN, SWIGLU>(p, lds, expert, n_tile, row0, row_end);
+    const int rem_rows = span - m_tile * 256;  // rows left from this tile on
+    if constexpr (SWIGLU) {
+        const int64_t col0 = static_cast<int64_t>(n_tile) * 128;
+        if (rem_rows > 128) fast_tile<4, WN, 256, true>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) fast_tile<2, WN, 256, true>(p, lds, expert, col0, row0, row_end);
+        else fast_tile<1, WN, 256, true>(p, lds, expert, col0, row0, row_end);
+    } else if (piece < 0) {
+        const int64_t col0 = static_cast<int64_t>(n_tile) * 256;
+        if (rem_rows > 128) fast_tile<4, WN, 256, false>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) fast_tile<2, WN, 256, false>(p, lds, expert, col0, row0, row_end);
+        else fast_tile<1, WN, 256, false>(p, lds, expert, col0, row0, row_end);
+    } else {
+        const int64_t col0 = static_cast<int64_t>(n_tile) * 256 + piece * 128;
+        if (rem_rows > 128) fast_tile<4, WN, 128, false>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) fast_tile<2, WN, 128, false>(p, lds, expert, col0, row0, row_end);
+        else fast_tile<1, WN, 128, false>(p, lds, expert, col0, row0, row_end);
+    }
 }
 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
+// Compute units of the current device, cached per device id.
+static int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
 static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     const int64_t out_per_tile = SWIGLU ? BN / 2 : BN;
@@ -511,6 +555,8 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     int64_t blocks = m_bound * p.n_tiles;
     blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
     if (blocks == 0) return MOE_OK;
+    p.n_cu = device_cu_count();
+    if (!SWIGLU) blocks += 2 * p.n_cu;  // room for the split tail pieces
     if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
     if (BM == 256 && BN == 256 && p.k % kBK == 0) {
         hipLaunchKernelGGL((grouped_gemm_fast_kernel<kFastWaveCols, SWIGLU>),
