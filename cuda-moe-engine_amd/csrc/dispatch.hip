@@ -1,6 +1,7 @@
 // Token transport kernels for gfx950: deterministic dispatch (per-chunk
-// histogram and stable ranks, a one-block scan, then a stable pack with fused
-// padding) and the atomic-free weighted combine. Plus the standalone SwiGLU
+// histogram and stable ranks, then a stable pack that rebuilds its prefix from
+// the small per-chunk table, with fused padding) and the atomic-free weighted
+// combine. Plus the standalone SwiGLU
 // kept for API parity.
 //
 // Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:13-93 (count, scan,
@@ -14,147 +15,75 @@
 
 namespace moe {
 
-// Assignments are grouped in chunks of kChunkTokens consecutive tokens.
-constexpr int kChunkTokens = 16;
-constexpr int kRankThreads = kChunkTokens * kMaxTopk;  // one thread per assignment
+// Assignments are grouped in chunks of chunk_tokens consecutive tokens (a
+// multiple of 16, chosen on the host so that n_chunks * E <= kPrefixMax).
+constexpr int kPrefixMax = 512;
+constexpr int kRankThreads = 1024;
 constexpr int kRankWaves = kRankThreads / kWave;
 
 // ---------------------------------------------------------------------------
-// Stage 1: per-chunk histogram and in-chunk stable rank (one block per chunk).
-// slots[p] <- rank of p among the chunk's earlier assignments to the same
-// expert (-1 for an out-of-range id); chunk_counts[c][e] <- assignments of
-// chunk c to expert e.
+// Stage 1: per-chunk histogram and in-chunk stable rank (one block per chunk,
+// rounds of 1024 assignments). slots[p] <- rank of p among the chunk's earlier
+// assignments to the same expert (-1 for an out-of-range id);
+// chunk_counts[c][e] <- assignments of chunk c to expert e.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
     const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
-    int32_t* __restrict__ chunk_counts, int64_t n_assign, int experts, int topk) {
+    int32_t* __restrict__ chunk_counts, int64_t n_assign, int experts, int64_t chunk_assign) {
+    __shared__ int running[kMaxExperts];
     __shared__ int wave_counts[kRankWaves][kMaxExperts];
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid % kWave;
     const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-    for (int i = tid; i < kRankWaves * kMaxExperts; i += kRankThreads) (&wave_counts[0][0])[i] = 0;
-    __syncthreads();
-    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kChunkTokens * topk;
-    const int64_t p = p0 + tid;
-    const bool valid = tid < kChunkTokens * topk && p < n_assign;
-    const int e = valid ? ids[p] : -1;
-    const bool in_range = valid && e >= 0 && e < experts;
-    // Lanes holding the same expert id: intersect 6 bit-plane ballots.
-    uint64_t same = __ballot(in_range);
+    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * chunk_assign;
+    const int64_t p1 = min(p0 + chunk_assign, n_assign);
+    if (tid < kMaxExperts) running[tid] = 0;
+    for (int64_t base = p0; base < p1; base += kRankThreads) {
+        for (int i = tid; i < kRankWaves * kMaxExperts; i += kRankThreads) (&wave_counts[0][0])[i] = 0;
+        __syncthreads();
+        const int64_t p = base + tid;
+        const bool valid = p < p1;
+        const int e = valid ? ids[p] : -1;
+        const bool in_range = valid && e >= 0 && e < experts;
+        // Lanes holding the same expert id: intersect 6 bit-plane ballots.
+        uint64_t same = __ballot(in_range);
 #pragma unroll
-    for (int b = 0; b < 6; ++b) {
-        const bool bit = (e >> b) & 1;
-        const uint64_t plane = __ballot(in_range && bit);
-        same &= bit ? plane : ~plane;
-    }
-    const int rank = __popcll(same & lanes_below);
-    if (in_range && rank == 0) wave_counts[wave][e] = __popcll(same);
-    __syncthreads();
-    if (valid) {
-        int s = -1;
-        if (in_range) {
-            s = rank;
-            for (int w = 0; w < wave; ++w) s += wave_counts[w][e];
+        for (int b = 0; b < 6; ++b) {
+            const bool bit = (e >> b) & 1;
+            const uint64_t plane = __ballot(in_range && bit);
+            same &= bit ? plane : ~plane;
         }
-        slots[p] = s;
-    }
-    if (tid < experts) {
-        int total = 0;
-        for (int w = 0; w < kRankWaves; ++w) total += wave_counts[w][tid];
-        chunk_counts[static_cast<int64_t>(blockIdx.x) * experts + tid] = total;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Stage 2 (one block): chunk_counts[c][e] -> exclusive prefix over chunks
-// (in place, the chunk's base slot for expert e), counts[e] = totals,
-// offsets[e+1] = offsets[e] + ceil(counts[e]/a)*a. 16 groups of 64 threads
-// each own a contiguous run of chunks; thread (g, e) walks its run twice.
-// ---------------------------------------------------------------------------
-constexpr int kScanGroups = 16;
-constexpr int kScanBatch = 32;
-
-__global__ __launch_bounds__(kScanGroups * kMaxExperts) void scan_kernel(
-    int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int n_chunks, int experts, int alignment) {
-    __shared__ int seg_sum[kScanGroups][kMaxExperts];
-    __shared__ int seg_base[kScanGroups][kMaxExperts];
-    const int tid = threadIdx.x;
-    const int e = tid % kMaxExperts;
-    const int g = tid / kMaxExperts;
-    const int per = (n_chunks + kScanGroups - 1) / kScanGroups;
-    const int c0 = g * per;
-    const int c1 = min(n_chunks, c0 + per);
-    // Loads are issued in batches of kScanBatch so each walk is not latency
-    // bound; the first batch stays in registers for the write-back phase.
-    int sum = 0;
-    int first[kScanBatch];
-#pragma unroll
-    for (int u = 0; u < kScanBatch; ++u)
-        first[u] = (e < experts && c0 + u < c1) ? chunk_counts[static_cast<int64_t>(c0 + u) * experts + e] : 0;
-#pragma unroll
-    for (int u = 0; u < kScanBatch; ++u) sum += first[u];
-    if (e < experts) {
-        for (int cb = c0 + kScanBatch; cb < c1; cb += kScanBatch) {
-            int v[kScanBatch];
-#pragma unroll
-            for (int u = 0; u < kScanBatch; ++u)
-                v[u] = (cb + u < c1) ? chunk_counts[static_cast<int64_t>(cb + u) * experts + e] : 0;
-#pragma unroll
-            for (int u = 0; u < kScanBatch; ++u) sum += v[u];
-        }
-    }
-    seg_sum[g][e] = sum;
-    __syncthreads();
-    if (tid < kMaxExperts) {
-        int running = 0;
-        for (int gg = 0; gg < kScanGroups; ++gg) {
-            seg_base[gg][tid] = running;
-            running += seg_sum[gg][tid];
-        }
-        // Wave 0: totals, aligned spans and their inclusive scan over experts.
-        const int total = tid < experts ? running : 0;
-        const int span = (total + alignment - 1) / alignment * alignment;
-        int incl = span;
-        for (int d = 1; d < kWave; d <<= 1) {
-            const int up = __shfl_up(incl, d);
-            if (tid >= d) incl += up;
-        }
-        if (tid < experts) {
-            counts[tid] = total;
-            offsets[tid + 1] = incl;
-        }
-        if (tid == 0) offsets[0] = 0;
-    }
-    __syncthreads();
-    if (e < experts) {
-        int running = seg_base[g][e];
-#pragma unroll
-        for (int u = 0; u < kScanBatch; ++u) {
-            if (c0 + u < c1) chunk_counts[static_cast<int64_t>(c0 + u) * experts + e] = running;
-            running += first[u];
-        }
-        for (int cb = c0 + kScanBatch; cb < c1; cb += kScanBatch) {
-            int v[kScanBatch];
-#pragma unroll
-            for (int u = 0; u < kScanBatch; ++u)
-                v[u] = (cb + u < c1) ? chunk_counts[static_cast<int64_t>(cb + u) * experts + e] : 0;
-#pragma unroll
-            for (int u = 0; u < kScanBatch; ++u) {
-                if (cb + u < c1) chunk_counts[static_cast<int64_t>(cb + u) * experts + e] = running;
-                running += v[u];
+        const int rank = __popcll(same & lanes_below);
+        if (in_range && rank == 0) wave_counts[wave][e] = __popcll(same);
+        __syncthreads();
+        if (valid) {
+            int s = -1;
+            if (in_range) {
+                s = running[e] + rank;
+                for (int w = 0; w < wave; ++w) s += wave_counts[w][e];
             }
+            slots[p] = s;
         }
+        __syncthreads();
+        if (tid < experts) {
+            int add = 0;
+            for (int w = 0; w < kRankWaves; ++w) add += wave_counts[w][tid];
+            running[tid] += add;
+        }
+        __syncthreads();
     }
+    if (tid < experts) chunk_counts[static_cast<int64_t>(blockIdx.x) * experts + tid] = running[tid];
 }
 
 // ---------------------------------------------------------------------------
-// Stage 3: pack. A block owns `pack_tokens` tokens of one chunk: slot = chunk
-// base + in-chunk rank, dest = offsets[e] + slot (inverse and slots written),
-// then each x row is read once and written to its K destinations with VB-byte
-// accesses, kLoads accesses in flight per thread. Blocks e, e+grid, ... zero
-// the padding rows of expert e.
+// Stage 2: prefix + pack + padding. A block owns `pack_tokens` tokens of one
+// chunk. From chunk_counts (at most kPrefixMax entries) it rebuilds the expert
+// totals (counts and aligned offsets, written by block 0) and the counts of
+// earlier chunks, turns in-chunk ranks into within-expert slots and
+// destinations (slots and inverse written), then reads each x row once and
+// writes it to its K destinations with VB-byte accesses, kPackLoads in flight
+// per thread. Blocks e, e+grid, ... zero the padding rows of expert e.
 // ---------------------------------------------------------------------------
 constexpr int kPackThreads = 256;
 constexpr int kPackMaxAssign = 128;  // pack_tokens * K upper bound
@@ -175,29 +104,77 @@ template <> __device__ __forceinline__ uint16_t zero_vec<uint16_t>() { return 0;
 template <int VB>
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
-    const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
-    int64_t tokens, int64_t row_bytes, int experts, int topk, int pack_tokens) {
+    const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
+    int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
+    int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2) {
     using V = typename VecOf<VB>::T;
+    __shared__ int part_all[kPackThreads / kWave][kMaxExperts];
+    __shared__ int part_before[kPackThreads / kWave][kMaxExperts];
+    __shared__ int total[kMaxExperts];
+    __shared__ int before[kMaxExperts];
+    __shared__ int offs[kMaxExperts + 1];
     __shared__ int64_t dest[kPackMaxAssign];
+
     const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * pack_tokens;
-    const int64_t chunk = t0 / kChunkTokens;
+    const int my_chunk = static_cast<int>(t0 / chunk_tokens);
+
+    // (a) Column sums of chunk_counts: all chunks, and chunks before mine.
+    //     Thread tid always sees expert tid % experts_pow2 (a divisor of 256).
+    {
+        const int e = tid % experts_pow2;
+        int s_all = 0, s_before = 0;
+        if (e < experts) {
+            for (int c = tid / experts_pow2; c < n_chunks; c += kPackThreads / experts_pow2) {
+                const int v = chunk_counts[static_cast<int64_t>(c) * experts + e];
+                s_all += v;
+                if (c < my_chunk) s_before += v;
+            }
+        }
+        for (int m = experts_pow2; m < kWave; m <<= 1) {
+            s_all += __shfl_xor(s_all, m);
+            s_before += __shfl_xor(s_before, m);
+        }
+        if (lane < experts_pow2) {
+            part_all[wave][lane] = s_all;
+            part_before[wave][lane] = s_before;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int tot = 0, bef = 0;
+        if (lane < experts) {
+            for (int w = 0; w < kPackThreads / kWave; ++w) {
+                tot += part_all[w][lane];
+                bef += part_before[w][lane];
+            }
+        }
+        const int span = (tot + alignment - 1) / alignment * alignment;
+        int incl = span;  // inclusive scan over the wavefront
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int up = __shfl_up(incl, d);
+            if (lane >= d) incl += up;
+        }
+        if (lane < experts) {
+            total[lane] = tot;
+            before[lane] = bef;
+            offs[lane + 1] = incl;
+        }
+        if (lane == 0) offs[0] = 0;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (tid < experts) counts[tid] = total[tid];
+        if (tid <= experts) offsets[tid] = offs[tid];
+    }
+
+    // (b) Destinations of this block's assignments.
     const int64_t t_end = min(t0 + pack_tokens, tokens);
     const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
     const int n_local = n_tok * topk;
-    const int64_t nv = row_bytes / VB;
-    // The first token's row loads do not depend on the destinations: issue them
-    // before the ids -> slots -> chunk base -> offsets chain.
-    V head[kPackLoads];
-    if (n_tok > 0) {
-        const V* src = reinterpret_cast<const V*>(x + t0 * row_bytes);
-#pragma unroll
-        for (int u = 0; u < kPackLoads; ++u) {
-            const int64_t v = tid + u * kPackThreads;
-            if (v < nv) head[u] = src[v];
-        }
-    }
     for (int i = tid; i < n_local; i += kPackThreads) {
         const int64_t pa = t0 * topk + i;
         const int e = ids[pa];
@@ -205,8 +182,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
         if (e >= 0 && e < experts) {
             const int r = slots[pa];
             if (r >= 0) {
-                const int slot = chunk_base[chunk * experts + e] + r;
-                d = static_cast<int64_t>(offsets[e]) + slot;
+                const int slot = before[e] + r;
+                d = static_cast<int64_t>(offs[e]) + slot;
                 slots[pa] = slot;
                 inverse[pa] = static_cast<int32_t>(d);
             }
@@ -215,21 +192,17 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     }
     __syncthreads();
 
-    // Row copies, token by token: each thread loads up to kPackLoads vectors of a
-    // row (256 apart) before storing them to the row's K destinations.
+    // (c) Row copies, token by token: each thread loads up to kPackLoads vectors
+    //     of a row (256 apart) before storing them to the row's K destinations.
+    const int64_t nv = row_bytes / VB;
     for (int tl = 0; tl < n_tok; ++tl) {
         const V* src = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes);
         for (int64_t vb = 0; vb < nv; vb += static_cast<int64_t>(kPackThreads) * kPackLoads) {
             V val[kPackLoads];
-            if (tl == 0 && vb == 0) {
 #pragma unroll
-                for (int u = 0; u < kPackLoads; ++u) val[u] = head[u];
-            } else {
-#pragma unroll
-                for (int u = 0; u < kPackLoads; ++u) {
-                    const int64_t v = vb + tid + u * kPackThreads;
-                    if (v < nv) val[u] = src[v];
-                }
+            for (int u = 0; u < kPackLoads; ++u) {
+                const int64_t v = vb + tid + u * kPackThreads;
+                if (v < nv) val[u] = src[v];
             }
             for (int k = 0; k < topk; ++k) {
                 const int64_t d = dest[tl * topk + k];
@@ -244,10 +217,10 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
         }
     }
 
-    // Padding rows [offsets[e] + counts[e], offsets[e+1]) are zero.
+    // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
     for (int e = blockIdx.x; e < experts; e += gridDim.x) {
-        const int64_t r0 = static_cast<int64_t>(offsets[e]) + counts[e];
-        const int64_t r1 = offsets[e + 1];
+        const int64_t r0 = offs[e] + total[e];
+        const int64_t r1 = offs[e + 1];
         const int64_t pad_items = (r1 - r0) * nv;
         V* out = reinterpret_cast<V*>(packed + r0 * row_bytes);
         for (int64_t i = tid; i < pad_items; i += kPackThreads) out[i] = zero_vec<V>();
@@ -355,19 +328,35 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const typename Elem<DT>::T*
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-static int64_t n_chunks_of(int64_t tokens) { return (tokens + kChunkTokens - 1) / kChunkTokens; }
+static int64_t pow2_at_least(int64_t v) {
+    int64_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// Smallest chunk (16 tokens times a power of two) with n_chunks * E <= kPrefixMax.
+static int64_t chunk_tokens_for(int64_t tokens, int64_t experts) {
+    int64_t chunk = 16;
+    while (chunk < tokens && ((tokens + chunk - 1) / chunk) * experts > kPrefixMax) chunk <<= 1;
+    return chunk;
+}
 
 int64_t dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
     (void)topk;
-    const int64_t n = n_chunks_of(tokens) * experts;
+    const int64_t chunk = chunk_tokens_for(tokens, experts);
+    const int64_t n = ((tokens + chunk - 1) / chunk) * experts;
     return (n > 0 ? n : 1) * static_cast<int64_t>(sizeof(int32_t));
 }
 
-// Tokens per pack block: the smallest power of two (dividing kChunkTokens)
-// whose rows reach 8 KiB, so many small blocks stay resident per CU.
+// Tokens per pack block: the smallest power of two whose rows reach
+// MOE_PACK_BLOCK_BYTES (chunks are multiples of 16 tokens, so a block never
+// straddles two chunks).
+#ifndef MOE_PACK_BLOCK_BYTES
+#define MOE_PACK_BLOCK_BYTES 8192
+#endif
 static int pack_tokens_for(int64_t row_bytes, int topk) {
     int pt = 1;
-    while (pt * 2 <= kChunkTokens && pt * 2 * topk <= kPackMaxAssign && pt * row_bytes < 8192) pt <<= 1;
+    while (pt * 2 <= 16 && pt * 2 * topk <= kPackMaxAssign && pt * row_bytes < MOE_PACK_BLOCK_BYTES) pt <<= 1;
     return pt;
 }
 
@@ -377,18 +366,15 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
                     int alignment, bool vectorized, hipStream_t stream) {
     const int64_t elem = dtype_size(dtype);
     const int64_t row_bytes = hidden * elem;
-    const int64_t n_chunks = n_chunks_of(tokens);
+    const int64_t chunk = chunk_tokens_for(tokens, experts);
+    const int64_t n_chunks = tokens > 0 ? (tokens + chunk - 1) / chunk : 0;
     const int64_t n_assign = tokens * topk;
     if (n_chunks > 0) {
         hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(n_chunks)), dim3(kRankThreads),
-                           0, stream, ids, slots, chunk_counts, n_assign, experts, topk);
+                           0, stream, ids, slots, chunk_counts, n_assign, experts, chunk * topk);
         const int rc = check_launch("count_rank_kernel");
         if (rc != MOE_OK) return rc;
     }
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanGroups * kMaxExperts), 0, stream, chunk_counts,
-                       counts, offsets, static_cast<int>(n_chunks), experts, alignment);
-    int rc = check_launch("scan_kernel");
-    if (rc != MOE_OK) return rc;
     int vb = static_cast<int>(elem);
     if (vectorized) {
         if (row_bytes % 16 == 0) vb = 16;
@@ -397,11 +383,13 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
     }
     const int pt = pack_tokens_for(row_bytes, topk);
     const int64_t blocks = tokens > 0 ? (tokens + pt - 1) / pt : 1;
-    const dim3 grid(static_cast<unsigned>(std::max<int64_t>(blocks, std::min<int64_t>(experts, 64))));
-#define MOE_PACK_CASE(VBV)                                                                     \
-    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                  \
-                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets, \
-                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk, pt)
+    const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
+    const dim3 grid(static_cast<unsigned>(blocks));
+#define MOE_PACK_CASE(VBV)                                                                       \
+    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                    \
+                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets,   \
+                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,    \
+                       alignment, chunk, pt, static_cast<int>(n_chunks), experts_pow2)
     switch (vb) {
         case 16: MOE_PACK_CASE(16); break;
         case 8: MOE_PACK_CASE(8); break;
