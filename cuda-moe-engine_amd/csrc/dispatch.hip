@@ -1,7 +1,7 @@
 // Token transport kernels for gfx950: deterministic dispatch (per-chunk
-// histogram and stable ranks, then a stable pack that rebuilds its prefix from
-// the small per-chunk table, with fused padding) and the atomic-free weighted
-// combine. Plus the standalone SwiGLU
+// histogram and stable ranks; destinations from the small per-chunk table,
+// with the padding rows zeroed; then a streaming row copy) and the
+// atomic-free weighted combine. Plus the standalone SwiGLU
 // kept for API parity.
 //
 // Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:13-93 (count, scan,
@@ -15,8 +15,8 @@
 
 namespace moe {
 
-// Assignments are grouped in chunks of chunk_tokens consecutive tokens (a
-// multiple of 16, chosen on the host so that n_chunks * E <= kPrefixMax).
+// Assignments are grouped in chunks of chunk_tokens consecutive tokens (16
+// times a power of two, chosen on the host so that n_chunks * E <= kPrefixMax).
 constexpr int kPrefixMax = 512;
 constexpr int kRankThreads = 1024;
 constexpr int kRankWaves = kRankThreads / kWave;
@@ -77,17 +77,14 @@ __global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2: prefix + pack + padding. A block owns `pack_tokens` tokens of one
-// chunk. From chunk_counts (at most kPrefixMax entries) it rebuilds the expert
-// totals (counts and aligned offsets, written by block 0) and the counts of
-// earlier chunks, turns in-chunk ranks into within-expert slots and
-// destinations (slots and inverse written), then reads each x row once and
-// writes it to its K destinations with VB-byte accesses, kPackLoads in flight
-// per thread. Blocks e, e+grid, ... zero the padding rows of expert e.
+// Stage 2: destinations. Every block loads the whole per-chunk table (at most
+// kPrefixMax entries) into LDS and turns it into exclusive per-chunk bases and
+// aligned expert offsets; then each thread finalises one assignment:
+// slot = base[chunk][e] + in-chunk rank, inverse = offsets[e] + slot. Block 0
+// writes counts and offsets; blocks e, e+grid, ... zero the padding rows of
+// expert e (rows [offsets[e] + counts[e], offsets[e+1])).
 // ---------------------------------------------------------------------------
-constexpr int kPackThreads = 256;
-constexpr int kPackMaxAssign = 128;  // pack_tokens * K upper bound
-constexpr int kPackLoads = 4;        // vectors per thread per pass
+constexpr int kDestThreads = 256;
 
 template <int VB> struct VecOf;
 template <> struct VecOf<16> { using T = uint4; };
@@ -102,128 +99,96 @@ template <> __device__ __forceinline__ uint32_t zero_vec<uint32_t>() { return 0u
 template <> __device__ __forceinline__ uint16_t zero_vec<uint16_t>() { return 0; }
 
 template <int VB>
-__global__ __launch_bounds__(kPackThreads) void pack_kernel(
-    const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
+__global__ __launch_bounds__(kDestThreads) void dest_kernel(
+    const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
     const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
-    int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
-    int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
-    int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2) {
+    int32_t* __restrict__ offsets, int32_t* __restrict__ inverse, char* __restrict__ packed,
+    int64_t n_assign, int64_t row_bytes, int experts, int topk, int alignment,
+    int64_t chunk_tokens, int n_chunks) {
     using V = typename VecOf<VB>::T;
-    __shared__ int part_all[kPackThreads / kWave][kMaxExperts];
-    __shared__ int part_before[kPackThreads / kWave][kMaxExperts];
+    __shared__ int base[kPrefixMax];
     __shared__ int total[kMaxExperts];
-    __shared__ int before[kMaxExperts];
     __shared__ int offs[kMaxExperts + 1];
-    __shared__ int64_t dest[kPackMaxAssign];
-
     const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid % kWave;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * pack_tokens;
-    const int my_chunk = static_cast<int>(t0 / chunk_tokens);
-
-    // (a) Column sums of chunk_counts: all chunks, and chunks before mine.
-    //     Thread tid always sees expert tid % experts_pow2 (a divisor of 256).
-    {
-        const int e = tid % experts_pow2;
-        int s_all = 0, s_before = 0;
-        if (e < experts) {
-            for (int c = tid / experts_pow2; c < n_chunks; c += kPackThreads / experts_pow2) {
-                const int v = chunk_counts[static_cast<int64_t>(c) * experts + e];
-                s_all += v;
-                if (c < my_chunk) s_before += v;
-            }
-        }
-        for (int m = experts_pow2; m < kWave; m <<= 1) {
-            s_all += __shfl_xor(s_all, m);
-            s_before += __shfl_xor(s_before, m);
-        }
-        if (lane < experts_pow2) {
-            part_all[wave][lane] = s_all;
-            part_before[wave][lane] = s_before;
-        }
-    }
+    const int table = n_chunks * experts;
+    for (int i = tid; i < table; i += kDestThreads) base[i] = chunk_counts[i];
     __syncthreads();
-    if (wave == 0) {
-        int tot = 0, bef = 0;
-        if (lane < experts) {
-            for (int w = 0; w < kPackThreads / kWave; ++w) {
-                tot += part_all[w][lane];
-                bef += part_before[w][lane];
+    if (tid < kWave) {
+        int running = 0;
+        if (tid < experts) {
+            for (int c = 0; c < n_chunks; ++c) {
+                const int v = base[c * experts + tid];
+                base[c * experts + tid] = running;
+                running += v;
             }
         }
-        const int span = (tot + alignment - 1) / alignment * alignment;
+        const int span = (running + alignment - 1) / alignment * alignment;
         int incl = span;  // inclusive scan over the wavefront
         for (int d = 1; d < kWave; d <<= 1) {
             const int up = __shfl_up(incl, d);
-            if (lane >= d) incl += up;
+            if (tid >= d) incl += up;
         }
-        if (lane < experts) {
-            total[lane] = tot;
-            before[lane] = bef;
-            offs[lane + 1] = incl;
+        if (tid < experts) {
+            total[tid] = running;
+            offs[tid + 1] = incl;
         }
-        if (lane == 0) offs[0] = 0;
+        if (tid == 0) offs[0] = 0;
     }
     __syncthreads();
     if (blockIdx.x == 0) {
         if (tid < experts) counts[tid] = total[tid];
         if (tid <= experts) offsets[tid] = offs[tid];
     }
-
-    // (b) Destinations of this block's assignments.
-    const int64_t t_end = min(t0 + pack_tokens, tokens);
-    const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
-    const int n_local = n_tok * topk;
-    for (int i = tid; i < n_local; i += kPackThreads) {
-        const int64_t pa = t0 * topk + i;
-        const int e = ids[pa];
-        int64_t d = -1;
-        if (e >= 0 && e < experts) {
-            const int r = slots[pa];
-            if (r >= 0) {
-                const int slot = before[e] + r;
-                d = static_cast<int64_t>(offs[e]) + slot;
-                slots[pa] = slot;
-                inverse[pa] = static_cast<int32_t>(d);
-            }
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kDestThreads + tid;
+    if (p < n_assign) {
+        const int e = ids[p];
+        const int r = slots[p];
+        if (e >= 0 && e < experts && r >= 0) {
+            const int c = static_cast<int>(p / (chunk_tokens * topk));
+            const int slot = base[c * experts + e] + r;
+            slots[p] = slot;
+            inverse[p] = offs[e] + slot;
         }
-        dest[i] = d;
     }
-    __syncthreads();
-
-    // (c) Row copies, token by token: each thread loads up to kPackLoads vectors
-    //     of a row (256 apart) before storing them to the row's K destinations.
     const int64_t nv = row_bytes / VB;
-    for (int tl = 0; tl < n_tok; ++tl) {
-        const V* src = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes);
-        for (int64_t vb = 0; vb < nv; vb += static_cast<int64_t>(kPackThreads) * kPackLoads) {
-            V val[kPackLoads];
-#pragma unroll
-            for (int u = 0; u < kPackLoads; ++u) {
-                const int64_t v = vb + tid + u * kPackThreads;
-                if (v < nv) val[u] = src[v];
-            }
-            for (int k = 0; k < topk; ++k) {
-                const int64_t d = dest[tl * topk + k];
-                if (d < 0) continue;
-                V* dst = reinterpret_cast<V*>(packed + d * row_bytes);
-#pragma unroll
-                for (int u = 0; u < kPackLoads; ++u) {
-                    const int64_t v = vb + tid + u * kPackThreads;
-                    if (v < nv) dst[v] = val[u];
-                }
-            }
-        }
-    }
-
-    // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
     for (int e = blockIdx.x; e < experts; e += gridDim.x) {
-        const int64_t r0 = offs[e] + total[e];
-        const int64_t r1 = offs[e + 1];
-        const int64_t pad_items = (r1 - r0) * nv;
+        const int64_t r0 = static_cast<int64_t>(offs[e]) + total[e];
+        const int64_t pad_items = (offs[e + 1] - r0) * nv;
         V* out = reinterpret_cast<V*>(packed + r0 * row_bytes);
-        for (int64_t i = tid; i < pad_items; i += kPackThreads) out[i] = zero_vec<V>();
+        for (int64_t i = tid; i < pad_items; i += kDestThreads) out[i] = zero_vec<V>();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 3: row copies. One thread per (token, kCopyVecs VB-byte vectors): the
+// row's loads do not wait for anything; the K destinations come from inverse
+// (skipped where slots marks an out-of-range id).
+// ---------------------------------------------------------------------------
+constexpr int kCopyVecs = 2;
+
+template <int VB>
+__global__ __launch_bounds__(256) void copy_rows_kernel(
+    const char* __restrict__ x, const int32_t* __restrict__ slots, const int32_t* __restrict__ inverse,
+    char* __restrict__ packed, int64_t tokens, int64_t row_bytes, int topk) {
+    using V = typename VecOf<VB>::T;
+    const int64_t nv = row_bytes / VB;
+    const int64_t groups = (nv + kCopyVecs - 1) / kCopyVecs;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t t = idx / groups;
+    if (t >= tokens) return;
+    const int64_t v0 = (idx - t * groups) * kCopyVecs;
+    const V* src = reinterpret_cast<const V*>(x + t * row_bytes);
+    V val[kCopyVecs];
+#pragma unroll
+    for (int u = 0; u < kCopyVecs; ++u)
+        if (v0 + u < nv) val[u] = src[v0 + u];
+    for (int k = 0; k < topk; ++k) {
+        const int64_t pa = t * topk + k;
+        if (slots[pa] < 0) continue;
+        V* dst = reinterpret_cast<V*>(packed + static_cast<int64_t>(inverse[pa]) * row_bytes);
+#pragma unroll
+        for (int u = 0; u < kCopyVecs; ++u)
+            if (v0 + u < nv) dst[v0 + u] = val[u];
     }
 }
 
@@ -328,12 +293,6 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const typename Elem<DT>::T*
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-static int64_t pow2_at_least(int64_t v) {
-    int64_t p = 1;
-    while (p < v) p <<= 1;
-    return p;
-}
-
 // Smallest chunk (16 tokens times a power of two) with n_chunks * E <= kPrefixMax.
 static int64_t chunk_tokens_for(int64_t tokens, int64_t experts) {
     int64_t chunk = 16;
@@ -346,18 +305,6 @@ int64_t dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
     const int64_t chunk = chunk_tokens_for(tokens, experts);
     const int64_t n = ((tokens + chunk - 1) / chunk) * experts;
     return (n > 0 ? n : 1) * static_cast<int64_t>(sizeof(int32_t));
-}
-
-// Tokens per pack block: the smallest power of two whose rows reach
-// MOE_PACK_BLOCK_BYTES (chunks are multiples of 16 tokens, so a block never
-// straddles two chunks).
-#ifndef MOE_PACK_BLOCK_BYTES
-#define MOE_PACK_BLOCK_BYTES 8192
-#endif
-static int pack_tokens_for(int64_t row_bytes, int topk) {
-    int pt = 1;
-    while (pt * 2 <= 16 && pt * 2 * topk <= kPackMaxAssign && pt * row_bytes < MOE_PACK_BLOCK_BYTES) pt <<= 1;
-    return pt;
 }
 
 int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts,
@@ -381,24 +328,30 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
         else if (row_bytes % 8 == 0) vb = 8;
         else if (row_bytes % 4 == 0) vb = 4;
     }
-    const int pt = pack_tokens_for(row_bytes, topk);
-    const int64_t blocks = tokens > 0 ? (tokens + pt - 1) / pt : 1;
-    const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
-    const dim3 grid(static_cast<unsigned>(blocks));
-#define MOE_PACK_CASE(VBV)                                                                       \
-    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                    \
-                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets,   \
-                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,    \
-                       alignment, chunk, pt, static_cast<int>(n_chunks), experts_pow2)
+    const int64_t dest_blocks = std::max<int64_t>((n_assign + kDestThreads - 1) / kDestThreads, 1);
+    const int64_t copy_threads = tokens * ((row_bytes / vb + kCopyVecs - 1) / kCopyVecs);
+    const dim3 copy_grid(static_cast<unsigned>((copy_threads + 255) / 256));
+#define MOE_DISPATCH_CASE(VBV)                                                                       \
+    hipLaunchKernelGGL(dest_kernel<VBV>, dim3(static_cast<unsigned>(dest_blocks)), dim3(kDestThreads), \
+                       0, stream, ids, slots, chunk_counts, counts, offsets, inverse,                  \
+                       static_cast<char*>(packed), n_assign, row_bytes, experts, topk, alignment,      \
+                       chunk, static_cast<int>(n_chunks));                                             \
+    rc = check_launch("dest_kernel");                                                                  \
+    if (rc != MOE_OK) return rc;                                                                       \
+    if (copy_threads > 0)                                                                              \
+        hipLaunchKernelGGL(copy_rows_kernel<VBV>, copy_grid, dim3(256), 0, stream,                     \
+                           static_cast<const char*>(x), slots, inverse, static_cast<char*>(packed),    \
+                           tokens, row_bytes, topk)
+    int rc = MOE_OK;
     switch (vb) {
-        case 16: MOE_PACK_CASE(16); break;
-        case 8: MOE_PACK_CASE(8); break;
-        case 4: MOE_PACK_CASE(4); break;
-        case 2: MOE_PACK_CASE(2); break;
+        case 16: MOE_DISPATCH_CASE(16); break;
+        case 8: MOE_DISPATCH_CASE(8); break;
+        case 4: MOE_DISPATCH_CASE(4); break;
+        case 2: MOE_DISPATCH_CASE(2); break;
         default: return fail(MOE_ERR_UNSUPPORTED, "row size %lld bytes", (long long)row_bytes);
     }
-#undef MOE_PACK_CASE
-    return check_launch("pack_kernel");
+#undef MOE_DISPATCH_CASE
+    return check_launch("copy_rows_kernel");
 }
 
 template <int DT, int VE>
