@@ -1,8 +1,8 @@
 // Token transport kernels for gfx950: deterministic dispatch (per-chunk
-// histogram and stable ranks; destinations from the small per-chunk table,
-// with the padding rows zeroed; then a streaming row copy) and the
-// atomic-free weighted combine. Plus the standalone SwiGLU
-// kept for API parity.
+// histogram and stable ranks, then one pack kernel that rebuilds the expert
+// prefix from the small per-chunk table, writes destinations, copies rows and
+// zeroes padding) and the atomic-free weighted combine. Plus the standalone
+// SwiGLU kept for API parity.
 //
 // Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:13-93 (count, scan,
 // pack, combine), :194-275 (aligned layout and padding), :277-323 (SwiGLU).
@@ -17,7 +17,7 @@ namespace moe {
 
 // Assignments are grouped in chunks of chunk_tokens consecutive tokens (16
 // times a power of two, chosen on the host so that n_chunks * E <= kPrefixMax).
-constexpr int kPrefixMax = 512;
+constexpr int kPrefixMax = 1024;
 constexpr int kRankThreads = 1024;
 constexpr int kRankWaves = kRankThreads / kWave;
 
@@ -77,14 +77,15 @@ __global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2: destinations. Every block loads the whole per-chunk table (at most
-// kPrefixMax entries) into LDS and turns it into exclusive per-chunk bases and
-// aligned expert offsets; then each thread finalises one assignment:
-// slot = base[chunk][e] + in-chunk rank, inverse = offsets[e] + slot. Block 0
-// writes counts and offsets; blocks e, e+grid, ... zero the padding rows of
-// expert e (rows [offsets[e] + counts[e], offsets[e+1])).
+// Stage 2: prefix + pack + padding. A block owns `pack_tokens` tokens of one
+// chunk. It rebuilds, from chunk_counts, the expert totals (-> counts and
+// aligned offsets, written by block 0) and the counts of earlier chunks, turns
+// in-chunk ranks into within-expert slots and destinations, and copies each
+// token row once from x to its K destinations with VB-byte accesses. Blocks
+// e, e+grid, ... also zero the padding rows of expert e.
 // ---------------------------------------------------------------------------
-constexpr int kDestThreads = 256;
+constexpr int kPackThreads = 256;
+constexpr int kPackMaxAssign = 256;  // pack_tokens * K upper bound
 
 template <int VB> struct VecOf;
 template <> struct VecOf<16> { using T = uint4; };
@@ -99,96 +100,116 @@ template <> __device__ __forceinline__ uint32_t zero_vec<uint32_t>() { return 0u
 template <> __device__ __forceinline__ uint16_t zero_vec<uint16_t>() { return 0; }
 
 template <int VB>
-__global__ __launch_bounds__(kDestThreads) void dest_kernel(
-    const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
+__global__ __launch_bounds__(kPackThreads) void pack_kernel(
+    const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
     const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
-    int32_t* __restrict__ offsets, int32_t* __restrict__ inverse, char* __restrict__ packed,
-    int64_t n_assign, int64_t row_bytes, int experts, int topk, int alignment,
-    int64_t chunk_tokens, int n_chunks) {
+    int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
+    int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
+    int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2) {
     using V = typename VecOf<VB>::T;
-    __shared__ int base[kPrefixMax];
+    __shared__ int part_all[kPackThreads / kWave][kMaxExperts];
+    __shared__ int part_before[kPackThreads / kWave][kMaxExperts];
     __shared__ int total[kMaxExperts];
+    __shared__ int before[kMaxExperts];
     __shared__ int offs[kMaxExperts + 1];
+    __shared__ int64_t dest[kPackMaxAssign];
+
     const int tid = threadIdx.x;
-    const int table = n_chunks * experts;
-    for (int i = tid; i < table; i += kDestThreads) base[i] = chunk_counts[i];
-    __syncthreads();
-    if (tid < kWave) {
-        int running = 0;
-        if (tid < experts) {
-            for (int c = 0; c < n_chunks; ++c) {
-                const int v = base[c * experts + tid];
-                base[c * experts + tid] = running;
-                running += v;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * pack_tokens;
+    const int my_chunk = static_cast<int>(t0 / chunk_tokens);
+
+    // (a) Column sums of chunk_counts: all chunks, and chunks before mine.
+    //     Thread tid always sees expert tid % experts_pow2 (a divisor of 256).
+    {
+        const int e = tid % experts_pow2;
+        int s_all = 0, s_before = 0;
+        if (e < experts) {
+            for (int c = tid / experts_pow2; c < n_chunks; c += kPackThreads / experts_pow2) {
+                const int v = chunk_counts[static_cast<int64_t>(c) * experts + e];
+                s_all += v;
+                if (c < my_chunk) s_before += v;
             }
         }
-        const int span = (running + alignment - 1) / alignment * alignment;
+        for (int m = experts_pow2; m < kWave; m <<= 1) {
+            s_all += __shfl_xor(s_all, m);
+            s_before += __shfl_xor(s_before, m);
+        }
+        if (lane < experts_pow2 && lane < kMaxExperts) {
+            part_all[wave][lane] = s_all;
+            part_before[wave][lane] = s_before;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int tot = 0, bef = 0;
+        if (lane < experts) {
+            for (int w = 0; w < kPackThreads / kWave; ++w) {
+                tot += part_all[w][lane];
+                bef += part_before[w][lane];
+            }
+        }
+        const int span = (tot + alignment - 1) / alignment * alignment;
         int incl = span;  // inclusive scan over the wavefront
         for (int d = 1; d < kWave; d <<= 1) {
             const int up = __shfl_up(incl, d);
-            if (tid >= d) incl += up;
+            if (lane >= d) incl += up;
         }
-        if (tid < experts) {
-            total[tid] = running;
-            offs[tid + 1] = incl;
+        if (lane < experts) {
+            total[lane] = tot;
+            before[lane] = bef;
+            offs[lane + 1] = incl;
         }
-        if (tid == 0) offs[0] = 0;
+        if (lane == 0) offs[0] = 0;
     }
     __syncthreads();
     if (blockIdx.x == 0) {
         if (tid < experts) counts[tid] = total[tid];
         if (tid <= experts) offsets[tid] = offs[tid];
     }
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * kDestThreads + tid;
-    if (p < n_assign) {
+
+    // (b) Destinations of this block's assignments.
+    const int64_t t_end = min(t0 + pack_tokens, tokens);
+    const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
+    const int n_local = n_tok * topk;
+    for (int i = tid; i < n_local; i += kPackThreads) {
+        const int64_t p = t0 * topk + i;
         const int e = ids[p];
-        const int r = slots[p];
-        if (e >= 0 && e < experts && r >= 0) {
-            const int c = static_cast<int>(p / (chunk_tokens * topk));
-            const int slot = base[c * experts + e] + r;
-            slots[p] = slot;
-            inverse[p] = offs[e] + slot;
+        int64_t d = -1;
+        if (e >= 0 && e < experts) {
+            const int r = slots[p];
+            if (r >= 0) {
+                const int slot = before[e] + r;
+                d = static_cast<int64_t>(offs[e]) + slot;
+                slots[p] = slot;
+                inverse[p] = static_cast<int32_t>(d);
+            }
+        }
+        dest[i] = d;
+    }
+    __syncthreads();
+
+    // (c) Row copies: each x row is read once and written to its K rows.
+    const int64_t nv = row_bytes / VB;
+    const int64_t items = static_cast<int64_t>(n_tok) * nv;
+    for (int64_t i = tid; i < items; i += kPackThreads) {
+        const int tl = static_cast<int>(i / nv);
+        const int64_t v = i - static_cast<int64_t>(tl) * nv;
+        const V val = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[v];
+        for (int k = 0; k < topk; ++k) {
+            const int64_t d = dest[tl * topk + k];
+            if (d >= 0) reinterpret_cast<V*>(packed + d * row_bytes)[v] = val;
         }
     }
-    const int64_t nv = row_bytes / VB;
+
+    // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
     for (int e = blockIdx.x; e < experts; e += gridDim.x) {
-        const int64_t r0 = static_cast<int64_t>(offs[e]) + total[e];
-        const int64_t pad_items = (offs[e + 1] - r0) * nv;
-        V* out = reinterpret_cast<V*>(packed + r0 * row_bytes);
-        for (int64_t i = tid; i < pad_items; i += kDestThreads) out[i] = zero_vec<V>();
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Stage 3: row copies. One thread per (token, kCopyVecs VB-byte vectors): the
-// row's loads do not wait for anything; the K destinations come from inverse
-// (skipped where slots marks an out-of-range id).
-// ---------------------------------------------------------------------------
-constexpr int kCopyVecs = 2;
-
-template <int VB>
-__global__ __launch_bounds__(256) void copy_rows_kernel(
-    const char* __restrict__ x, const int32_t* __restrict__ slots, const int32_t* __restrict__ inverse,
-    char* __restrict__ packed, int64_t tokens, int64_t row_bytes, int topk) {
-    using V = typename VecOf<VB>::T;
-    const int64_t nv = row_bytes / VB;
-    const int64_t groups = (nv + kCopyVecs - 1) / kCopyVecs;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t t = idx / groups;
-    if (t >= tokens) return;
-    const int64_t v0 = (idx - t * groups) * kCopyVecs;
-    const V* src = reinterpret_cast<const V*>(x + t * row_bytes);
-    V val[kCopyVecs];
-#pragma unroll
-    for (int u = 0; u < kCopyVecs; ++u)
-        if (v0 + u < nv) val[u] = src[v0 + u];
-    for (int k = 0; k < topk; ++k) {
-        const int64_t pa = t * topk + k;
-        if (slots[pa] < 0) continue;
-        V* dst = reinterpret_cast<V*>(packed + static_cast<int64_t>(inverse[pa]) * row_bytes);
-#pragma unroll
-        for (int u = 0; u < kCopyVecs; ++u)
-            if (v0 + u < nv) dst[v0 + u] = val[u];
+        const int64_t r0 = offs[e] + total[e];
+        const int64_t r1 = offs[e + 1];
+        const int64_t pad_items = (r1 - r0) * nv;
+        V* base = reinterpret_cast<V*>(packed + r0 * row_bytes);
+        for (int64_t i = tid; i < pad_items; i += kPackThreads) base[i] = zero_vec<V>();
     }
 }
 
@@ -293,17 +314,38 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const typename Elem<DT>::T*
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-// Smallest chunk (16 tokens times a power of two) with n_chunks * E <= kPrefixMax.
-static int64_t chunk_tokens_for(int64_t tokens, int64_t experts) {
+struct DispatchPlan {
+    int64_t chunk_tokens;
+    int64_t n_chunks;
+    int pack_tokens;
+    int64_t pack_blocks;
+};
+
+static int64_t pow2_at_least(int64_t v) {
+    int64_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// Chunk size keeps n_chunks * E <= kPrefixMax (each pack block rebuilds its
+// prefix from the whole chunk_counts table); pack blocks move about 16 KiB of rows.
+static DispatchPlan plan_dispatch(int64_t tokens, int64_t experts, int64_t topk, int64_t row_bytes) {
+    DispatchPlan p{};
     int64_t chunk = 16;
     while (chunk < tokens && ((tokens + chunk - 1) / chunk) * experts > kPrefixMax) chunk <<= 1;
-    return chunk;
+    p.chunk_tokens = chunk;
+    p.n_chunks = tokens > 0 ? (tokens + chunk - 1) / chunk : 0;
+    int64_t pt = 1;
+    const int64_t max_pt = kPackMaxAssign / topk;
+    while (pt * 2 <= max_pt && pt * 2 <= chunk && pt * row_bytes < 16384) pt <<= 1;
+    p.pack_tokens = static_cast<int>(pt);
+    p.pack_blocks = tokens > 0 ? (tokens + pt - 1) / pt : 1;
+    return p;
 }
 
 int64_t dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
-    (void)topk;
-    const int64_t chunk = chunk_tokens_for(tokens, experts);
-    const int64_t n = ((tokens + chunk - 1) / chunk) * experts;
+    const DispatchPlan p = plan_dispatch(tokens, experts, topk, 16);
+    const int64_t n = p.n_chunks * experts;
     return (n > 0 ? n : 1) * static_cast<int64_t>(sizeof(int32_t));
 }
 
@@ -313,13 +355,13 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
                     int alignment, bool vectorized, hipStream_t stream) {
     const int64_t elem = dtype_size(dtype);
     const int64_t row_bytes = hidden * elem;
-    const int64_t chunk = chunk_tokens_for(tokens, experts);
-    const int64_t n_chunks = tokens > 0 ? (tokens + chunk - 1) / chunk : 0;
+    const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes);
     const int64_t n_assign = tokens * topk;
-    if (n_chunks > 0) {
-        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(n_chunks)), dim3(kRankThreads),
-                           0, stream, ids, slots, chunk_counts, n_assign, experts, chunk * topk);
-        const int rc = check_launch("count_rank_kernel");
+    if (plan.n_chunks > 0) {
+        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)),
+                           dim3(kRankThreads), 0, stream, ids, slots, chunk_counts, n_assign,
+                           experts, plan.chunk_tokens * topk);
+        int rc = check_launch("count_rank_kernel");
         if (rc != MOE_OK) return rc;
     }
     int vb = static_cast<int>(elem);
@@ -328,30 +370,23 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
         else if (row_bytes % 8 == 0) vb = 8;
         else if (row_bytes % 4 == 0) vb = 4;
     }
-    const int64_t dest_blocks = std::max<int64_t>((n_assign + kDestThreads - 1) / kDestThreads, 1);
-    const int64_t copy_threads = tokens * ((row_bytes / vb + kCopyVecs - 1) / kCopyVecs);
-    const dim3 copy_grid(static_cast<unsigned>((copy_threads + 255) / 256));
-#define MOE_DISPATCH_CASE(VBV)                                                                       \
-    hipLaunchKernelGGL(dest_kernel<VBV>, dim3(static_cast<unsigned>(dest_blocks)), dim3(kDestThreads), \
-                       0, stream, ids, slots, chunk_counts, counts, offsets, inverse,                  \
-                       static_cast<char*>(packed), n_assign, row_bytes, experts, topk, alignment,      \
-                       chunk, static_cast<int>(n_chunks));                                             \
-    rc = check_launch("dest_kernel");                                                                  \
-    if (rc != MOE_OK) return rc;                                                                       \
-    if (copy_threads > 0)                                                                              \
-        hipLaunchKernelGGL(copy_rows_kernel<VBV>, copy_grid, dim3(256), 0, stream,                     \
-                           static_cast<const char*>(x), slots, inverse, static_cast<char*>(packed),    \
-                           tokens, row_bytes, topk)
-    int rc = MOE_OK;
+    const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
+    const dim3 grid(static_cast<unsigned>(plan.pack_blocks));
+#define MOE_PACK_CASE(VBV)                                                                   \
+    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                \
+                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets, \
+                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,  \
+                       alignment, plan.chunk_tokens, plan.pack_tokens,                        \
+                       static_cast<int>(plan.n_chunks), experts_pow2)
     switch (vb) {
-        case 16: MOE_DISPATCH_CASE(16); break;
-        case 8: MOE_DISPATCH_CASE(8); break;
-        case 4: MOE_DISPATCH_CASE(4); break;
-        case 2: MOE_DISPATCH_CASE(2); break;
+        case 16: MOE_PACK_CASE(16); break;
+        case 8: MOE_PACK_CASE(8); break;
+        case 4: MOE_PACK_CASE(4); break;
+        case 2: MOE_PACK_CASE(2); break;
         default: return fail(MOE_ERR_UNSUPPORTED, "row size %lld bytes", (long long)row_bytes);
     }
-#undef MOE_DISPATCH_CASE
-    return check_launch("copy_rows_kernel");
+#undef MOE_PACK_CASE
+    return check_launch("pack_kernel");
 }
 
 template <int DT, int VE>
