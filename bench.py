@@ -39,6 +39,11 @@ CONFIGS = {
     "c3_t4096": (4096, 1024, 2048, 16, 2, "balanced"),
     "c5": (8192, 2048, 1408, 64, 6, "zipf"),
 }
+# Standalone transport (dispatch + combine only): tokens, hidden, experts, topk, alignment.
+TRANSPORT_CONFIGS = {"c2_transport": (4096, 2048, 8, 2, 1)}
+# HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs, scaled by the
+# same counters read on a copy of known size (written next to the kernel summaries).
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
 
 
 def parse_args(argv=None):
@@ -46,10 +51,12 @@ def parse_args(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c4_t4096", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c4_t4096", choices=sorted(CONFIGS) + sorted(TRANSPORT_CONFIGS))
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="time a 1 GiB device-to-device copy (the counter scale for traffic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch-variant", action="store_true")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=4)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=2048)
     return ap.parse_args(argv)
 
 
@@ -59,54 +66,43 @@ def _events(n):
     return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
 
 
+def time_loop(fn, steps, warmup):
+    """Mean time of one call (us): `steps` back-to-back calls between two events on the
+    current stream (the stream every kernel of this package is launched on)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) * 1000.0 / steps
+
+
 def time_stages(block, x, steps, warmup):
-    """Per-stage event timing; every event is recorded on the stream the kernels use."""
+    """Per-stage mean latency: each stage repeated back to back on its own inputs
+    (every stage is idempotent given the previous stage's outputs)."""
     import torch
 
     state = block.workspace(x)
-    stages = {}
-
-    def route():
-        stages["_route"] = block.route(x)
-
-    def dispatch():
-        ids32, ids64, _ = stages["_route"]
-        state.transport.dispatch(x, ids32, ids64)
-
     ext = block._extension
-
-    def gateup():
-        ext.gateup_swiglu_out(state.transport.packed, block.gate_up_weight, state.transport.offsets,
-                              state.activated)
-
-    def down():
-        ext.grouped_gemm_out(state.activated, block.down_weight, state.transport.offsets,
-                             state.expert_output)
-
-    def combine():
-        state.transport.combine(state.expert_output, stages["_route"][2])
-
-    order = [("router", route), ("dispatch", dispatch), ("gateup_swiglu", gateup), ("down", down),
-             ("combine", combine)]
     with torch.inference_mode():
-        for _ in range(warmup):
-            for _, fn in order:
-                fn()
-        torch.cuda.synchronize()
-        ev = {name: _events(steps) for name, _ in order}
-        for i in range(steps):
-            for name, fn in order:
-                s, e = ev[name][i]
-                s.record()
-                fn()
-                e.record()
-        torch.cuda.synchronize()
-    out = {}
-    for name, _ in order:
-        samples = [s.elapsed_time(e) * 1000.0 for s, e in ev[name]]
-        out[name] = {"mean_us": statistics.fmean(samples), "median_us": statistics.median(samples),
-                     "min_us": min(samples)}
-    return out
+        ids32, ids64, weights = block.route(x)
+        state.transport.dispatch(x, ids32, ids64)
+        stages = {
+            "router": lambda: block.route(x),
+            "dispatch": lambda: state.transport.dispatch(x, ids32, ids64),
+            "gateup_swiglu": lambda: ext.gateup_swiglu_out(state.transport.packed, block.gate_up_weight,
+                                                           state.transport.offsets, state.activated),
+            "down": lambda: ext.grouped_gemm_out(state.activated, block.down_weight, state.transport.offsets,
+                                                 state.expert_output),
+            "combine": lambda: state.transport.combine(state.expert_output, weights),
+        }
+        return {name: {"mean_us": time_loop(fn, steps, warmup)} for name, fn in stages.items()}
 
 
 def cpu_baseline(block, x, sample_tokens):
@@ -141,9 +137,12 @@ def cpu_baseline(block, x, sample_tokens):
         def __getitem__(self, e):
             return self.d[e]
 
+    gu_w = _W(gate_up, tuple(block.gate_up_weight.shape))
+    dn_w = _W(down, tuple(block.down_weight.shape))
+    # Untimed warm-up on two tokens (first touch of the weight pages, BLAS start-up).
+    oracle.token_major_forward(sample[:2], gu_w, dn_w, ids[:2], weights[:2])
     t1 = time.perf_counter()
-    oracle.token_major_forward(sample, _W(gate_up, tuple(block.gate_up_weight.shape)),
-                               _W(down, tuple(block.down_weight.shape)), ids, weights)
+    oracle.token_major_forward(sample, gu_w, dn_w, ids, weights)
     compute_s = time.perf_counter() - t1 + (t1 - t0 - convert_s)
     per_token_us = compute_s * 1e6 / sample_tokens
     return {
@@ -171,12 +170,125 @@ def torch_variant_gpu(cfg, weights, x, steps, warmup):
     return {"median_us": stats["median_us"], "min_us": stats["min_us"], "gemm_backend": kind}
 
 
+def measured_traffic(config, kernels):
+    """Scaled HBM bytes per launch of `kernels` at `config`, if a counter run recorded them."""
+    try:
+        table = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    total = 0
+    for kernel in kernels:
+        entry = table.get(config, {}).get(kernel)
+        if not entry:
+            return None
+        total += entry.get("fetch_bytes", 0) + entry.get("write_bytes", 0)
+    return total
+
+
+def copy_calibration(steps):
+    """1 GiB device-to-device copy: reads and writes exactly 2^30 bytes per launch."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    us = s.elapsed_time(e) * 1000.0 / steps
+    print(json.dumps({"copy_bytes_each_way": n, "avg_us": round(us, 2),
+                      "gbs_read_plus_write": round(2 * n / (us * 1e-6) / 1e9, 1)}), flush=True)
+    return 0
+
+
+def transport_bench(args):
+    """Standalone dispatch + combine (ops-level transport) on one GPU."""
+    import torch
+
+    from moe_dispatch.routing import make_transport_case
+    from moe_dispatch.workspace import CudaWorkspace
+    from oracle import moe_oracle as oracle
+
+    tokens, hidden, experts, topk, alignment = TRANSPORT_CONFIGS[args.config]
+    torch.cuda.set_device(0)
+    x, ids32, ids64, weights = make_transport_case(tokens, hidden, experts, topk, torch.bfloat16, seed=0)
+    ws = CudaWorkspace(tokens, hidden, experts, topk, torch.bfloat16, alignment=alignment)
+    y = torch.randn(ws.capacity_rows, hidden, device="cuda",
+                    generator=torch.Generator(device="cuda").manual_seed(1)).bfloat16()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            ws.dispatch(x, ids32, ids64)
+            ws.combine(y, weights)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            ws.dispatch(x, ids32, ids64)
+            ws.combine(y, weights)
+        end.record()
+        torch.cuda.synchronize()
+    mean_us = start.elapsed_time(end) * 1000.0 / args.steps
+        d_us = time_loop(lambda: ws.dispatch(x, ids32, ids64), args.steps, args.warmup)
+        c_us = time_loop(lambda: ws.combine(y, weights), args.steps, args.warmup)
+    pad_rows = int(ws.offsets[-1].item()) - tokens * topk
+    disp_bytes = oracle.dispatch_bytes(tokens, hidden, topk, pad_rows)
+    comb_bytes = oracle.combine_bytes(tokens, hidden, topk)
+    d_gbs = disp_bytes / (d_us * 1e-6) / 1e9
+    c_gbs = comb_bytes / (c_us * 1e-6) / 1e9
+    traffic = measured_traffic(args.config, ("count_rank_kernel", "pack_kernel<16>"))
+    result = {
+        "metric": "MoE block fwd latency (us) + expert TFLOP/s % bf16 MFMA peak; dispatch GB/s",
+        "value": round(mean_us, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_us / 1000.0, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) rows, uniform random expert ids, softmax weights)",
+        "config": {"workload": f"standalone dispatch+combine {args.config}: T={tokens} H={hidden} "
+                               f"E={experts} top-{topk} alignment={alignment}",
+                   "tokens": tokens, "hidden": hidden, "experts": experts, "topk": topk,
+                   "alignment": alignment},
+        "stages_us": {"dispatch": round(d_us, 2), "combine": round(c_us, 2)},
+        "dispatch_gbs": round(d_gbs, 1),
+        "combine_gbs": round(c_gbs, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "count_rank_kernel + pack_kernel (one dispatch call)",
+            "achieved": round(d_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(d_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": disp_bytes,
+            "avg_launch_us": round(d_us, 2),
+        },
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are out of scope",
                           "n_gpus": args.gpus}))
         return 2
+    if args.copy_calibration:
+        return copy_calibration(args.steps)
+    if args.config in TRANSPORT_CONFIGS:
+        return transport_bench(args)
     import numpy as np
     import torch
 
@@ -211,7 +323,7 @@ def main(argv=None):
     step_us = [s.elapsed_time(e) * 1000.0 for s, e in per_step]
     mean_us = total_ms * 1000.0 / args.steps
 
-    stages = time_stages(block, x, args.steps, min(args.warmup, 3))
+    stages = time_stages(block, x, args.steps, max(min(args.warmup, 3), 1))
     counts = block.workspace(x).transport.counts.cpu().numpy()
     offsets = block.workspace(x).transport.offsets.cpu().numpy()
     n_assign = tokens * topk
@@ -251,12 +363,12 @@ def main(argv=None):
         "expert_counts": counts.tolist(),
         "roofline": {
             "bound": "mfma",
-            "kernel": "grouped_gemm_kernel<SWIGLU> (gate/up + SwiGLU)",
+            "kernel": "grouped_gemm_fast_kernel<4, true> (gate/up GEMM + SwiGLU epilogue)",
             "achieved": round(gu_tflops, 1),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gu_tflops / BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config, ("grouped_gemm_fast_kernel<4, true>",)),
             "flop_per_launch": gateup_flop,
             "avg_launch_us": round(t_gu, 2),
         },

@@ -162,3 +162,87 @@ def test_config4_decode_sizes_full_model_shape(tokens):
     """H=4096, I=14336, E=8, top-2 at decode token counts, full weights."""
     _check_block(MoEConfig(4096, 14336, 8, 2), tokens, seed=1, large_i=True)
     torch.cuda.empty_cache()
+
+
+def _sample_rows(offsets, counts, per_expert, rng):
+    """First, last and random rows of every non-empty expert span; sample offsets."""
+    rows, sample_offsets = [], [0]
+    for e in range(len(counts)):
+        s, n = int(offsets[e]), int(counts[e])
+        if n:
+            pick = {0, n - 1} | set(rng.integers(0, n, size=max(per_expert - 2, 0)).tolist())
+            rows.extend(s + r for r in sorted(pick))
+        sample_offsets.append(len(rows))
+    return np.asarray(rows, dtype=np.int64), np.asarray(sample_offsets, dtype=np.int64)
+
+
+def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, token_sample=48, seed=0):
+    """Full-size block: exact layout and permutation over all tokens; GEMMs, combine and
+    end-to-end output on sampled rows/tokens (rows of a GEMM are independent)."""
+    block, x, out, ids32, weights, state = _run_block(cfg, tokens, "balanced", seed, bias)
+    rng = np.random.default_rng(seed)
+    transport = state.transport
+    ids, w = to_np(ids32), to_np(weights)
+    # Routing on a token sample against exact logits (near-ties excepted).
+    tsample = np.sort(rng.choice(tokens, size=min(token_sample, tokens), replace=False))
+    router_w, bias_np = to_np(block.router_weight), to_np(block.routing_bias)
+    xs = to_np(x[torch.from_numpy(tsample).cuda()])
+    logits = oracle.router_logits(xs, router_w)
+    ids_ref, w_ref, _ = oracle.topk_route(logits, bias_np, cfg.topk)
+    safe = route_margin(logits, bias_np, cfg.topk) > 1e-4
+    np.testing.assert_array_equal(ids[tsample][safe], ids_ref[safe])
+    np.testing.assert_allclose(w[tsample][safe], w_ref[safe], rtol=0, atol=2e-5)
+    # Dispatch over every token: layout bit-exact, permutation and padding.
+    layout = oracle.dispatch_layout(ids, cfg.experts, cfg.alignment)
+    np.testing.assert_array_equal(to_np(transport.counts), layout["counts"])
+    np.testing.assert_array_equal(to_np(transport.offsets), layout["offsets"])
+    np.testing.assert_array_equal(to_np(transport.inverse), layout["inverse"])
+    np.testing.assert_array_equal(to_np(transport.slots).reshape(-1), layout["slots"])
+    inv = transport.inverse.reshape(-1).long()
+    gathered = transport.packed.index_select(0, inv).view(tokens, cfg.topk, cfg.hidden)
+    assert torch.equal(gathered, x[:, None, :].expand_as(gathered))
+    offsets, counts = layout["offsets"], layout["counts"]
+    for e in range(cfg.experts):
+        pad = transport.packed[int(offsets[e]) + int(counts[e]):int(offsets[e + 1])]
+        assert int(torch.count_nonzero(pad)) == 0
+    # Expert GEMMs on sampled rows of every expert, each on the kernels' own input.
+    rows, sample_offsets = _sample_rows(offsets, counts, per_expert, rng)
+    rows_t = torch.from_numpy(rows).cuda()
+    gate_up, down = LazyExpertWeights(block.gate_up_weight), LazyExpertWeights(block.down_weight)
+    packed_s = to_np(transport.packed.index_select(0, rows_t))
+    act_s = to_np(state.activated.index_select(0, rows_t))
+    proj_ref = oracle.bf16_round(oracle.grouped_gemm(packed_s, gate_up, sample_offsets))
+    assert_near_bit_exact(act_s, oracle.swiglu(proj_ref, len(rows)), max_fraction=2e-4, max_steps=2.0)
+    eo_s = to_np(state.expert_output.index_select(0, rows_t))
+    eo_ref = oracle.bf16_round(oracle.grouped_gemm(act_s, down, sample_offsets))
+    assert_near_bit_exact(eo_s, eo_ref, max_fraction=1e-4)
+    # Combine on sampled tokens, bit-exact on the kernels' expert output.
+    inv_s = layout["inverse"][tsample]
+    needed = np.unique(inv_s)
+    eo_rows = np.zeros((transport.capacity_rows, cfg.hidden), np.float32)
+    eo_rows[needed] = to_np(state.expert_output.index_select(0, torch.from_numpy(needed).cuda()))
+    got = to_np(out)[tsample]
+    np.testing.assert_array_equal(got, oracle.combine(eo_rows, inv_s, w[tsample]))
+    # End to end on the token sample against the exact-arithmetic token-major oracle.
+    dense = oracle.token_major_forward(to_np(x), gate_up, down, ids, w, token_index=tsample, order="exact")
+    assert float(np.abs(got - dense).max()) <= MAX_ABS
+    assert rel_l2(got, dense) <= (REL_L2_LARGE_I if large_i else REL_L2)
+    return counts
+
+
+def test_config4_prefill_full_size_sampled():
+    """C4 at T=4096 (the benchmark workload): full layout, sampled GEMM rows and tokens."""
+    _check_block_sampled(MoEConfig(4096, 14336, 8, 2), 4096, large_i=True)
+
+
+def test_config3_t4096_full_size_sampled():
+    _check_block_sampled(MoEConfig(1024, 2048, 16, 2), 4096)
+
+
+def test_config5_full_size_zipf_skew():
+    """C5: T=8192, H=2048, I=1408, E=64, top-6 with the Zipf router bias: several experts
+    get no tokens and a few take more than 15% of the assignments."""
+    cfg = MoEConfig(2048, 1408, 64, 6)
+    counts = _check_block_sampled(cfg, 8192, bias=oracle.zipf_bias(64))
+    assert int((counts == 0).sum()) >= 3
+    assert int((counts > 0.15 * 8192 * 6).sum()) >= 2
