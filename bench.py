@@ -234,9 +234,9 @@ def transport_bench(args):
             ws.combine(y, weights)
         end.record()
         torch.cuda.synchronize()
-    mean_us = start.elapsed_time(end) * 1000.0 / args.steps
         d_us = time_loop(lambda: ws.dispatch(x, ids32, ids64), args.steps, args.warmup)
         c_us = time_loop(lambda: ws.combine(y, weights), args.steps, args.warmup)
+    mean_us = start.elapsed_time(end) * 1000.0 / args.steps
     pad_rows = int(ws.offsets[-1].item()) - tokens * topk
     disp_bytes = oracle.dispatch_bytes(tokens, hidden, topk, pad_rows)
     comb_bytes = oracle.combine_bytes(tokens, hidden, topk)

@@ -1,0 +1,42 @@
+"""bench.py on the CPU: it imports, refuses more than one GPU, and reads counter traffic."""
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import bench
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_bench_refuses_multi_gpu():
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
+                          text=True, timeout=120)
+    assert proc.returncode == 2
+    assert "one GPU" in json.loads(proc.stdout.strip())["error"]
+
+
+def test_bench_configs_and_defaults():
+    args = bench.parse_args([])
+    assert args.gpus == 1 and args.config == "c4_t4096"
+    assert bench.CONFIGS["c4_t4096"][:5] == (4096, 4096, 14336, 8, 2)
+    assert bench.TRANSPORT_CONFIGS["c2_transport"] == (4096, 2048, 8, 2, 1)
+    assert bench.parse_args(["--config", "c2_transport"]).config == "c2_transport"
+
+
+def test_measured_traffic_sums_kernels(tmp_path, monkeypatch):
+    table = {"cfg": {"a": {"fetch_bytes": 10, "write_bytes": 5}, "b": {"fetch_bytes": 1, "write_bytes": 2}}}
+    path = tmp_path / "traffic.json"
+    path.write_text(json.dumps(table))
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", path)
+    assert bench.measured_traffic("cfg", ("a",)) == 15
+    assert bench.measured_traffic("cfg", ("a", "b")) == 18
+    assert bench.measured_traffic("cfg", ("missing",)) is None
+    assert bench.measured_traffic("other", ("a",)) is None
+
+
+def test_committed_traffic_table_covers_the_bench_kernels():
+    table = json.loads((ROOT / "profiles" / "hbm_traffic.json").read_text())
+    assert "grouped_gemm_fast_kernel<4, true>" in table["c4_t4096"]
+    assert {"count_rank_kernel", "pack_kernel<16>"} <= set(table["c2_transport"])
