@@ -363,12 +363,12 @@ def main(argv=None):
         "expert_counts": counts.tolist(),
         "roofline": {
             "bound": "mfma",
-            "kernel": "grouped_gemm_fast_kernel<4, true> (gate/up GEMM + SwiGLU epilogue)",
+            "kernel": "grouped_gemm_ring_kernel<true> (gate/up GEMM + SwiGLU epilogue)",
             "achieved": round(gu_tflops, 1),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gu_tflops / BF16_PEAK_TFLOPS, 4),
-            "traffic": measured_traffic(args.config, ("grouped_gemm_fast_kernel<4, true>",)),
+            "traffic": measured_traffic(args.config, ("grouped_gemm_ring_kernel<true>",)),
             "flop_per_launch": gateup_flop,
             "avg_launch_us": round(t_gu, 2),
         },

@@ -10,18 +10,21 @@
 // same lane, so the activation is computed in registers.
 //
 // Design (gfx950):
-//  * Block tile BM x BN x 64, 4 wavefronts in a WAVES_M x WAVES_N grid, each
-//    wave owns (BM/WAVES_M) x (BN/WAVES_N) as 32x32 MFMA sub-tiles; the fp32
-//    accumulators live in the AGPR/VGPR file (one wave per SIMD).
-//  * Global -> register -> LDS double buffering with one barrier per k-step.
-//    LDS rows are 128 bytes; 16-byte chunks are XOR-swizzled per row (swz) so
-//    both the 16-byte stores and the MFMA fragment reads are conflict free.
+//  * Fast path (K % 32 == 0, the block's shapes): ring_tile / grouped_gemm_ring_kernel
+//    below -- 256 x 256 tiles on four wavefronts of 128 x 128, direct-to-LDS
+//    buffer loads into a four-stage LDS ring, loads three k-steps ahead, MFMAs
+//    interleaved with fragment reads and loads, XCD-aware two-phase tile order.
+//  * Generic path (any K % 8 == 0): grouped_gemm_kernel -- global -> register ->
+//    LDS double buffering with one barrier per 64-wide k-step; LDS rows are 128
+//    bytes with 16-byte chunks XOR-swizzled per row (swz).
 //  * Tile schedule is built on the device from offsets: expert e contributes
-//    ceil(span_e/BM) x n_tiles tiles (0 for an empty expert). The grid is a
-//    host-side upper bound; surplus workgroups exit at once.
-//  * XCD-aware order: workgroup i runs on XCD i % 8, so logical tiles are
-//    remapped to give each XCD a contiguous range; inside an expert tiles go
-//    N-major so the row tiles of one expert share each weight slice in L2.
+//    ceil(span_e/256) row tiles per column tile (0 for an empty expert). The grid
+//    is a host-side upper bound; surplus workgroups exit at once, and no offsets
+//    are read on the host.
+//  * Every output element is one MFMA chain in ascending k with one fp32
+//    accumulator, whichever path and tile shape computes it.
+#include <type_traits>
+
 #include "moe_common.h"
 
 namespace moe {
@@ -254,22 +257,38 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 }
 
 // ---------------------------------------------------------------------------
-// Fast path (K % 64 == 0): 256 x 256 x 64 tiles fed by direct-to-LDS buffer
-// loads (buffer_load_dwordx4 ... lds). Each wavefront load moves 8 LDS rows
-// (1 KiB); lane l lands at byte 16*l of that block, i.e. row l/8, physical
-// chunk l%8, so it fetches the logical chunk that the swizzle maps there. Buffer resources bound the valid bytes: rows past the
-// expert's span and weight rows past the expert read as zero without
-// per-lane predicates. The last row tile of an expert is 64, 128 or 256 rows
-// high (the smallest that holds the remainder), so skewed and ragged spans do
-// not pay for a full 256-row tile. The k order of the MFMA chain (ascending,
-// one accumulator) is the same as the generic path.
+// Fast path (K % 32 == 0): 256 x 256 output tiles computed by four wavefronts
+// (one per SIMD), each owning 128 x 128 (or (TM/2) x (BNT/2) for the short last
+// row tile of an expert and the split tail pieces).
+//
+//  * Operands reach LDS through direct-to-LDS buffer loads
+//    (buffer_load_dwordx4 ... lds): a wavefront load moves 16 rows of 64 bytes
+//    (1 KiB), lane l landing at byte 16*l, i.e. row l/4, physical chunk l%4, so
+//    it fetches the logical chunk the swizzle maps there. Buffer resources
+//    bound the valid bytes: rows past the expert's span and weight rows past the
+//    expert read as zero with no per-lane predicate.
+//  * LDS is a ring of four stages of 32 k (A 16 KiB + B 16 KiB each). The loads
+//    of k-step kt+3 are issued while k-step kt computes, and the one barrier per
+//    k-step waits only for the stage about to be read (vmcnt leaves the two
+//    younger stages in flight), so global latency hides behind three k-steps.
+//  * Rows of 64 bytes hold 4 chunks of 16 bytes; chunk c of row r sits at
+//    physical chunk c ^ ((r >> 2) & 3), so 16 lanes reading 16 consecutive rows
+//    at one chunk touch all 64 banks once (conflict free).
+//  * Inside a k16 slice every MFMA is followed by at most one fragment read of
+//    the next slice and by its share of the next loads; fragments are read A
+//    and B alternately and the next slice's MFMAs run in order of the later of
+//    their two fragments, so each read has about a slice of MFMA work to land.
+//    sched_barrier fences pin this order.
+//  * The k order of each output's MFMA chain (ascending k, one accumulator) is
+//    the same as the generic path, whatever the tile shape.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format
-constexpr int kFastStage = (256 + 256) * kBK;  // bf16 elements per LDS stage (A then B)
-#ifndef MOE_FAST_WAVE_COLS
-#define MOE_FAST_WAVE_COLS 4
-#endif
-constexpr int kFastWaveCols = MOE_FAST_WAVE_COLS;  // 4 -> 8 wavefronts per tile
+constexpr int kRingK = 32;                     // k per LDS stage
+constexpr int kRingStages = 4;
+constexpr int kRingThreads = 256;
+constexpr uint32_t kRingAStage = 256 * kRingK * 2;            // bytes of one A (or B) stage
+constexpr uint32_t kRingBBase = kRingStages * kRingAStage;    // B stages follow the A stages
+constexpr uint32_t kRingBytes = 2 * kRingStages * kRingAStage;  // 128 KiB
 
 // Resource descriptor from wave-uniform values, pinned to SGPRs with readfirstlane
 // so buffer instructions take it directly (no waterfall loop).
@@ -282,34 +301,57 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              kRsrcWord3);
 }
 
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint16_t* lds_dst, uint32_t voffset,
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst, uint32_t voffset,
                                       uint32_t soffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rsrc, (__attribute__((address_space(3))) void*)(lds_dst), 16, voffset, soffset,
         0, 0);
 }
 
-// WN wave columns x 2 wave rows; WN = 4 gives 8 wavefronts (2 per SIMD), each
-// owning (TM/2) x 64, so one wave's stalls are covered by the other's MFMAs.
-// BNT weight rows per tile (256, or 128 for the split tail pieces); col0 is the
-// first output column of the tile.
-template <int SMT, int WN, int BNT, bool SWIGLU>
-__device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, int expert, int64_t col0,
+// s_waitcnt vmcnt(VM) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] in bits 3:0 and
+// vmcnt[5:4] in bits 15:14, expcnt in bits 6:4 with 7 = no wait, lgkmcnt in bits 11:8).
+template <int VM>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4));
+}
+// Workgroup barrier without the implied wait for all memory operations (the
+// explicit wait above bounds what must have landed); the memory clobber keeps
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ int ring_key(int row) { return (row >> 2) & 3; }
+
+// silu(g) * u for the fused epilogue: hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32; about 1 ulp each), g and u already rounded to bf16.
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+    return (g * u) * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// One output tile: rows [row0, row0 + SMT*64) of one expert (clamped to
+// row_end) by BNT weight rows starting at output column col0.
+template <int SMT, int BNT, bool SWIGLU>
+__device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end) {
-    constexpr int WAVES = 2 * WN;
-    constexpr int TM = SMT * 64;        // rows of this tile (2 wave rows x SMT x 32)
+    constexpr int WAVES = kRingThreads / kWave;
+    constexpr int TM = SMT * 64;
     constexpr int WTM = TM / 2;
-    constexpr int WTN = BNT / WN;
+    constexpr int WTN = BNT / 2;
     constexpr int SN = WTN / 32;
-    constexpr int A_LOADS = TM / 8 / WAVES;   // 8-row wavefront loads per wave
-    constexpr int B_LOADS = BNT / 8 / WAVES;
+    constexpr int A_LOADS = TM / 16 / WAVES;
+    constexpr int B_LOADS = BNT / 16 / WAVES;
+    constexpr int LOADS = A_LOADS + B_LOADS;
+    constexpr int H0 = LOADS / 2, H1 = LOADS - H0;
+    constexpr int NR = SMT + SN;      // fragment reads per k16 slice
+    constexpr int NM = SMT * SN;      // MFMAs per k16 slice
+    constexpr int kMin = SMT < SN ? SMT : SN;
     static_assert(A_LOADS >= 1 && B_LOADS >= 1 && SN >= 1, "tile shape");
     static_assert(!SWIGLU || SN % 2 == 0, "gate/up pairing needs an even sub-tile count");
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN;
-    const int wn = wave % WN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / 2;
+    const int wn = wave % 2;
     const int64_t K = p.k;
 
     const int64_t a_rows = min<int64_t>(row_end - row0, TM);
@@ -317,22 +359,22 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
     const __amdgpu_buffer_rsrc_t rsrc_b =
         make_rsrc(p.b + static_cast<int64_t>(expert) * p.nb * K, static_cast<uint32_t>(p.nb * K * 2));
 
-    // Lane l of an 8-row wavefront load lands at row r0 + l/8, physical chunk l%8,
-    // so it fetches logical chunk (l%8) ^ swz_key(row).
-    const int lrow = lane >> 3;
+    const int lrow = lane >> 2;
     uint32_t a_off[A_LOADS], b_off[B_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-        const int r = (wave * A_LOADS + i) * 8 + lrow;
-        const int lchunk = (lane & 7) ^ swz_key(r);
+        const int r = (wave * A_LOADS + i) * 16 + lrow;
+        const int lchunk = (lane & 3) ^ ring_key(r);
         a_off[i] = static_cast<uint32_t>((r * K + lchunk * 8) * 2);
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-        const int r = (wave * B_LOADS + i) * 8 + lrow;
-        const int lchunk = (lane & 7) ^ swz_key(r);
+        const int r = (wave * B_LOADS + i) * 16 + lrow;
+        const int lchunk = (lane & 3) ^ ring_key(r);
         int64_t brow;
         if constexpr (SWIGLU) {
+            // Wave column wc owns gate columns [wc*WTN/2, (wc+1)*WTN/2) of the
+            // tile and the matching up rows (I further on).
             const int wcol = r / WTN, w = r % WTN;
             constexpr int HALF = WTN / 2;
             const int64_t col = col0 + wcol * HALF + (w % HALF);
@@ -342,16 +384,39 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
         }
         b_off[i] = static_cast<uint32_t>((brow * K + lchunk * 8) * 2);
     }
-
-    auto issue = [&](int kt, int stage) {
-        const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2;
-        uint16_t* sa = lds + stage * kFastStage;
-        uint16_t* sb = sa + 256 * kBK;
+    // Loads [first, first + count) of the A-then-B list for k-step kt into stage st.
+    auto issue = [&](int kt, int st, int first, int count) {
+        const uint32_t koff = static_cast<uint32_t>(kt) * kRingK * 2;
 #pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) dma16(rsrc_a, sa + (wave * A_LOADS + i) * 8 * kBK, a_off[i], koff);
-#pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) dma16(rsrc_b, sb + (wave * B_LOADS + i) * 8 * kBK, b_off[i], koff);
+        for (int i = 0; i < LOADS; ++i) {
+            if (i < first || i >= first + count) continue;
+            if (i < A_LOADS)
+                dma16(rsrc_a, lds + st * kRingAStage + (wave * A_LOADS + i) * 1024, a_off[i], koff);
+            else
+                dma16(rsrc_b, lds + kRingBBase + st * kRingAStage + (wave * B_LOADS + (i - A_LOADS)) * 1024,
+                      b_off[i - A_LOADS], koff);
+        }
     };
+
+    // Fragment byte addresses in stage 0 for the two k16 slices of a stage; a
+    // stage switch adds a constant offset.
+    const int frag_row = lane & 31;
+    const int frag_half = lane >> 5;
+    uint32_t ra[2][SMT], rb[2][SN];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const int chunk = kk * 2 + frag_half;
+#pragma unroll
+        for (int i = 0; i < SMT; ++i) {
+            const int r = wm * WTM + i * 32 + frag_row;
+            ra[kk][i] = static_cast<uint32_t>((r * kRingK + ((chunk ^ ring_key(r)) << 3)) * 2);
+        }
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            const int r = wn * WTN + j * 32 + frag_row;
+            rb[kk][j] = kRingBBase + static_cast<uint32_t>((r * kRingK + ((chunk ^ ring_key(r)) << 3)) * 2);
+        }
+    }
 
     floatx16 acc[SMT][SN];
 #pragma unroll
@@ -361,72 +426,92 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int frag_row = lane & 31;
-    const int frag_half = lane >> 5;
-    const int k_steps = static_cast<int>(K / kBK);
-
-    // Fragment reads of one 16-wide k slice and the MFMAs that consume them.
-    auto read = [&](const uint16_t* sa, const uint16_t* sb, int kk, bf16x8_t (&fa)[SMT], bf16x8_t (&fb)[SN]) {
-        const int chunk = kk * 2 + frag_half;
-#pragma unroll
-        for (int i = 0; i < SMT; ++i) {
-            const int r = wm * WTM + i * 32 + frag_row;
-            fa[i] = *reinterpret_cast<const bf16x8_t*>(&sa[swz(r, chunk)]);
-        }
-#pragma unroll
-        for (int j = 0; j < SN; ++j) {
-            const int r = wn * WTN + j * 32 + frag_row;
-            fb[j] = *reinterpret_cast<const bf16x8_t*>(&sb[swz(r, chunk)]);
-        }
+    // Read slot r: A and B fragments alternate while both remain.
+    auto slot_is_a = [](int r) { return r < 2 * kMin ? (r % 2 == 0) : (SMT > SN); };
+    auto slot_index = [](int r) { return r < 2 * kMin ? r / 2 : (r - 2 * kMin) + kMin; };
+    auto read_slot = [&](auto st_c, int kk, int r, bf16x8_t (&fa)[SMT], bf16x8_t (&fb)[SN]) {
+        constexpr uint32_t kOff = decltype(st_c)::value * kRingAStage;
+        const int idx = slot_index(r);
+        if (slot_is_a(r)) fa[idx] = *reinterpret_cast<const bf16x8_t*>(lds + ra[kk][idx] + kOff);
+        else fb[idx] = *reinterpret_cast<const bf16x8_t*>(lds + rb[kk][idx] + kOff);
     };
-    // Weights fragment as src0, activations as src1: the 32x32 result comes out
-    // transposed, so lane l holds row l%32 and, in registers 4q..4q+3, the four
-    // consecutive columns 8q + 4*(l/32) + 0..3 (packed 8-byte stores). The
-    // products and their k grouping are unchanged.
-    auto mma = [&](const bf16x8_t (&fa)[SMT], const bf16x8_t (&fb)[SN]) {
-#pragma unroll
-        for (int i = 0; i < SMT; ++i)
-#pragma unroll
-            for (int j = 0; j < SN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-    };
-    // sched_barrier(0) fences keep each phase in place: the fragment reads of
-    // slice kk+1 are issued before the MFMAs of slice kk, so LDS latency hides
-    // under the matrix pipe and two fragment sets stay live.
+    // MFMA order within a slice: by the later read slot of its two fragments.
+    struct Order { int i[NM]; int j[NM]; };
+    constexpr Order order = [] {
+        Order o{};
+        int n = 0;
+        for (int s = 0; s < NR; ++s)
+            for (int i = 0; i < SMT; ++i)
+                for (int j = 0; j < SN; ++j) {
+                    const int ai = i < kMin ? 2 * i : 2 * kMin + (i - kMin);
+                    const int bj = j < kMin ? 2 * j + 1 : 2 * kMin + (j - kMin);
+                    if ((ai > bj ? ai : bj) == s) { o.i[n] = i; o.j[n] = j; ++n; }
+                }
+        return o;
+    }();
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
 
+    // Weights fragment as src0, activations as src1: the 32x32 result comes out
+    // transposed, so lane l holds row l%32 and, in registers 4q..4q+3, the four
+    // consecutive columns 8q + 4*(l/32) + 0..3 (packed 8-byte stores).
     bf16x8_t fa0[SMT], fb0[SN], fa1[SMT], fb1[SN];
-    issue(0, 0);
-    __syncthreads();
-    read(lds, lds + 256 * kBK, 0, fa0, fb0);
-    for (int kt = 0; kt < k_steps; ++kt) {
-        const int stage = kt & 1;
-        const uint16_t* sa = lds + stage * kFastStage;
-        const uint16_t* sb = sa + 256 * kBK;
-        const uint16_t* na = lds + (stage ^ 1) * kFastStage;
-        const uint16_t* nb = na + 256 * kBK;
-        // Next tile into the other stage (the last step reloads the final tile,
-        // keeping the body branch free; the copy is never read).
-        issue(min(kt + 1, k_steps - 1), stage ^ 1);
-        read(sa, sb, 1, fa1, fb1);
+    auto slice = [&](const bf16x8_t (&ca)[SMT], const bf16x8_t (&cb)[SN], bf16x8_t (&na)[SMT],
+                     bf16x8_t (&nb)[SN], auto rs_c, int rkk, int lkt, int lst, int first, int count) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            acc[order.i[m]][order.j[m]] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                cb[order.j[m]], ca[order.i[m]], acc[order.i[m]][order.j[m]], 0, 0, 0);
+            const int r0 = NR <= NM ? (m < NR ? m : NR) : m * NR / NM;
+            const int r1 = NR <= NM ? (m < NR ? m + 1 : NR) : (m + 1) * NR / NM;
+#pragma unroll
+            for (int r = r0; r < r1; ++r) read_slot(rs_c, rkk, r, na, nb);
+            const int q0 = m * count / NM, q1 = (m + 1) * count / NM;
+            if (q1 > q0) issue(lkt, lst, first + q0, q1 - q0);
+            fence();
+        }
+    };
+    const int k_steps = static_cast<int>(K / kRingK);
+    // k-step kt in stage ST (slice 0 already in fa0/fb0). Its loads of k-step
+    // kt+3 go to stage (ST+3)%4, whose reads all ended before the previous barrier.
+    auto step = [&](int kt, auto st_c) {
+        constexpr int ST = decltype(st_c)::value;
+        using NX = std::integral_constant<int, (ST + 1) % kRingStages>;
+        const int ahead = min(kt + 3, k_steps - 1);
+        constexpr int LST = (ST + 3) % kRingStages;
         fence();
-        mma(fa0, fb0);
+        slice(fa0, fb0, fa1, fb1, st_c, 1, ahead, LST, 0, H0);
+        // k-step kt+1 has landed once at most k-step kt+2's loads and this
+        // step's first part are younger.
+        wait_vm_lgkm0<LOADS + H0>();
+        ring_barrier();
         fence();
-        read(sa, sb, 2, fa0, fb0);
-        fence();
-        mma(fa1, fb1);
-        fence();
-        read(sa, sb, 3, fa1, fb1);
-        fence();
-        mma(fa0, fb0);
-        fence();
-        // All waves are done with this stage's fragments and the next stage has landed.
-        __syncthreads();
-        read(na, nb, 0, fa0, fb0);
-        fence();
-        mma(fa1, fb1);
-        fence();
+        slice(fa1, fb1, fa0, fb0, NX{}, 0, ahead, LST, H0, H1);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    // Surplus loads past the last k-step repeat it (same bytes, unread stage),
+    // which keeps the per-step load count and the vmcnt bound uniform.
+    issue(0, 0, 0, LOADS);
+    issue(min(1, k_steps - 1), 1, 0, LOADS);
+    issue(min(2, k_steps - 1), 2, 0, LOADS);
+    wait_vm_lgkm0<2 * LOADS>();
+    ring_barrier();
+    fence();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) read_slot(S0{}, 0, r, fa0, fb0);
+    int kt = 0;
+    for (; kt + 3 < k_steps; kt += 4) {
+        step(kt, S0{});
+        step(kt + 1, S1{});
+        step(kt + 2, S2{});
+        step(kt + 3, S3{});
     }
+    if (kt < k_steps) step(kt, S0{});
+    if (kt + 1 < k_steps) step(kt + 1, S1{});
+    if (kt + 2 < k_steps) step(kt + 2, S2{});
+    wait_vm_lgkm0<0>();
 
     // Epilogue: one row per lane, four consecutive columns per 8-byte store.
     const int col4 = 4 * (lane >> 5);
@@ -447,9 +532,7 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         const uint32_t gu = pack_bf16x2(acc[i][j][4 * q + t], acc[i][j + SN / 2][4 * q + t]);
-                        const float g = __uint_as_float(gu << 16);
-                        const float u = __uint_as_float(gu & 0xffff0000u);
-                        act[t] = silu_f32(g) * u;
+                        act[t] = swiglu_fast(__uint_as_float(gu << 16), __uint_as_float(gu & 0xffff0000u));
                     }
                     *reinterpret_cast<uint2*>(crow + col) =
                         make_uint2(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]));
@@ -472,60 +555,106 @@ __device__ __forceinline__ void fast_tile(const GemmParams& p, uint16_t* lds, in
     }
 }
 
-// Work list: full tiles in XCD-aware order, then (plain GEMM only) the tail.
-// When the last round of full tiles would occupy at most half of the CUs,
-// those tiles are split into two 128-column pieces each; every piece still
-// runs the whole k chain in order, so results are unchanged.
-template <int WN, bool SWIGLU>
-__global__ __launch_bounds__(128 * WN) void grouped_gemm_fast_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * kFastStage];
+// Work list, built on the device from offsets. Row tiles of more than 128 rows
+// form phase 1 (equal cost) and the short last row tile of an expert (at most
+// 128 rows) forms phase 2, so the CUs of an XCD run phase-1 tiles in lockstep
+// rounds and share A and B k-slices in L2. Inside a phase, tiles go expert by
+// expert, column tile by column tile, row tiles fastest, and each phase is
+// spread over the XCDs in contiguous ranges (workgroup i runs on XCD i % 8).
+// For the plain GEMM a short last round of a phase (at most half of the CUs)
+// is split into 128-column pieces; every piece still runs the whole k chain
+// in order, so results do not change.
+struct RingPhase {
+    int count;   // tiles
+    int main;    // tiles mapped XCD-contiguously
+    int blocks;  // workgroups of the main part (multiple of 8)
+    int pieces;  // split tail pieces (2 per split tile)
+};
+
+__device__ __forceinline__ RingPhase ring_phase(int count, int n_cu, bool allow_split) {
+    RingPhase ph;
+    ph.count = count;
+    const int rem = n_cu > 0 ? count % n_cu : 0;
+    const bool split = allow_split && rem > 0 && 2 * rem <= n_cu;
+    ph.main = split ? count - rem : count;
+    ph.blocks = (ph.main + kNumXcd - 1) / kNumXcd * kNumXcd;
+    ph.pieces = split ? 2 * rem : 0;
+    return ph;
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(kRingThreads) void grouped_gemm_ring_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) char lds[kRingBytes];
     const int32_t* __restrict__ offs = p.offsets;
-    int total = 0;
-    for (int e = 0; e < p.experts; ++e) total += ((offs[e + 1] - offs[e] + 255) / 256) * p.n_tiles;
-    const int rem = p.n_cu > 0 ? total % p.n_cu : 0;
-    const bool split = !SWIGLU && rem > 0 && 2 * rem <= p.n_cu;
-    const int main_tiles = split ? total - rem : total;
-    const int per_xcd = (main_tiles + kNumXcd - 1) / kNumXcd;
-    int tile, piece = -1;
-    if (static_cast<int>(blockIdx.x) < kNumXcd * per_xcd) {
-        tile = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
-        if (tile >= main_tiles) return;
-    } else {
-        const int q = blockIdx.x - kNumXcd * per_xcd;
-        if (!split || q >= 2 * rem) return;
-        tile = main_tiles + q / 2;
-        piece = q % 2;
+    auto full_tiles = [](int span) { return span / 256 + ((span % 256) > 128 ? 1 : 0); };
+    int n_full = 0, n_part = 0;
+    for (int e = 0; e < p.experts; ++e) {
+        const int span = offs[e + 1] - offs[e];
+        const int mf = full_tiles(span);
+        n_full += mf * p.n_tiles;
+        n_part += ((span + 255) / 256 - mf) * p.n_tiles;
     }
-    int expert = 0, base = 0, m_tiles = 0, span = 0;
+    const RingPhase ph1 = ring_phase(n_full, p.n_cu, !SWIGLU);
+    const RingPhase ph2 = ring_phase(n_part, p.n_cu, !SWIGLU);
+    int q = blockIdx.x;
+    int phase = -1, tile = 0, piece = -1;
+    const RingPhase* phs[2] = {&ph1, &ph2};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const RingPhase& ph = *phs[k];
+        if (phase >= 0) break;
+        if (q < ph.blocks) {
+            const int per = ph.blocks / kNumXcd;
+            tile = (q % kNumXcd) * per + q / kNumXcd;
+            if (tile >= ph.main) return;
+            phase = k;
+        } else if (q < ph.blocks + ph.pieces) {
+            const int r = q - ph.blocks;
+            tile = ph.main + r / 2;
+            piece = r % 2;
+            phase = k;
+        } else {
+            q -= ph.blocks + ph.pieces;
+        }
+    }
+    if (phase < 0) return;
+    int expert = 0, base = 0, span = 0, mf = 0;
     for (; expert < p.experts; ++expert) {
         span = offs[expert + 1] - offs[expert];
-        m_tiles = (span + 255) / 256;
-        const int t = m_tiles * p.n_tiles;
+        mf = full_tiles(span);
+        const int t = (phase == 0 ? mf : (span + 255) / 256 - mf) * p.n_tiles;
         if (tile < base + t) break;
         base += t;
     }
+    if (expert >= p.experts) return;
     const int rel = tile - base;
-    const int n_tile = rel / m_tiles;
-    const int m_tile = rel - n_tile * m_tiles;
+    int n_tile, m_tile;
+    if (phase == 0) {
+        n_tile = rel / mf;
+        m_tile = rel - n_tile * mf;
+    } else {
+        n_tile = rel;
+        m_tile = mf;
+    }
     const int64_t row0 = offs[expert] + static_cast<int64_t>(m_tile) * 256;
     const int64_t row_end = min(static_cast<int64_t>(offs[expert + 1]), p.rows);
     if (row0 < 0 || row0 >= row_end) return;
     const int rem_rows = span - m_tile * 256;  // rows left from this tile on
     if constexpr (SWIGLU) {
         const int64_t col0 = static_cast<int64_t>(n_tile) * 128;
-        if (rem_rows > 128) fast_tile<4, WN, 256, true>(p, lds, expert, col0, row0, row_end);
-        else if (rem_rows > 64) fast_tile<2, WN, 256, true>(p, lds, expert, col0, row0, row_end);
-        else fast_tile<1, WN, 256, true>(p, lds, expert, col0, row0, row_end);
+        if (rem_rows > 128) ring_tile<4, 256, true>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) ring_tile<2, 256, true>(p, lds, expert, col0, row0, row_end);
+        else ring_tile<1, 256, true>(p, lds, expert, col0, row0, row_end);
     } else if (piece < 0) {
         const int64_t col0 = static_cast<int64_t>(n_tile) * 256;
-        if (rem_rows > 128) fast_tile<4, WN, 256, false>(p, lds, expert, col0, row0, row_end);
-        else if (rem_rows > 64) fast_tile<2, WN, 256, false>(p, lds, expert, col0, row0, row_end);
-        else fast_tile<1, WN, 256, false>(p, lds, expert, col0, row0, row_end);
+        if (rem_rows > 128) ring_tile<4, 256, false>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) ring_tile<2, 256, false>(p, lds, expert, col0, row0, row_end);
+        else ring_tile<1, 256, false>(p, lds, expert, col0, row0, row_end);
     } else {
         const int64_t col0 = static_cast<int64_t>(n_tile) * 256 + piece * 128;
-        if (rem_rows > 128) fast_tile<4, WN, 128, false>(p, lds, expert, col0, row0, row_end);
-        else if (rem_rows > 64) fast_tile<2, WN, 128, false>(p, lds, expert, col0, row0, row_end);
-        else fast_tile<1, WN, 128, false>(p, lds, expert, col0, row0, row_end);
+        if (rem_rows > 128) ring_tile<4, 128, false>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) ring_tile<2, 128, false>(p, lds, expert, col0, row0, row_end);
+        else ring_tile<1, 128, false>(p, lds, expert, col0, row0, row_end);
     }
 }
 
@@ -553,16 +682,19 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     // Upper bound on row tiles: sum_e ceil(span_e/BM) <= ceil(R/BM) + E.
     const int64_t m_bound = (rows + BM - 1) / BM + p.experts;
     int64_t blocks = m_bound * p.n_tiles;
-    blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
     if (blocks == 0) return MOE_OK;
     p.n_cu = device_cu_count();
-    if (!SWIGLU) blocks += 2 * p.n_cu;  // room for the split tail pieces
-    if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
-    if (BM == 256 && BN == 256 && p.k % kBK == 0) {
-        hipLaunchKernelGGL((grouped_gemm_fast_kernel<kFastWaveCols, SWIGLU>),
-                           dim3(static_cast<unsigned>(blocks)), dim3(128 * kFastWaveCols), 0, stream, p);
-        return check_launch("grouped_gemm_fast_kernel");
+    if (BM == 256 && BN == 256 && p.k % kRingK == 0) {
+        // Two phases, each rounded up to the XCD count, plus room for the split
+        // tail pieces (at most n_cu per phase).
+        int64_t ring_blocks = blocks + 2 * kNumXcd;
+        if (!SWIGLU) ring_blocks += 2 * static_cast<int64_t>(p.n_cu);
+        if (ring_blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
+        hipLaunchKernelGGL((grouped_gemm_ring_kernel<SWIGLU>), dim3(static_cast<unsigned>(ring_blocks)),
+                           dim3(kRingThreads), 0, stream, p);
+        return check_launch("grouped_gemm_ring_kernel");
     }
+    if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
     hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, SWIGLU>),
                        dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads), 0, stream, p);
     return check_launch("grouped_gemm_kernel");

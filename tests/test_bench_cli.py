@@ -38,5 +38,5 @@ def test_measured_traffic_sums_kernels(tmp_path, monkeypatch):
 
 def test_committed_traffic_table_covers_the_bench_kernels():
     table = json.loads((ROOT / "profiles" / "hbm_traffic.json").read_text())
-    assert "grouped_gemm_fast_kernel<4, true>" in table["c4_t4096"]
+    assert "grouped_gemm_ring_kernel<true>" in table["c4_t4096"]
     assert {"count_rank_kernel", "pack_kernel<16>"} <= set(table["c2_transport"])
