@@ -56,6 +56,7 @@ def parse_args(argv=None):
                     help="time a 1 GiB device-to-device copy (the counter scale for traffic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch-variant", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replay timing")
     ap.add_argument("--cpu-sample-tokens", type=int, default=2048)
     return ap.parse_args(argv)
 
@@ -324,6 +325,12 @@ def main(argv=None):
     mean_us = total_ms * 1000.0 / args.steps
 
     stages = time_stages(block, x, args.steps, max(min(args.warmup, 3), 1))
+    graph_us = None
+    if not args.no_graph:
+        from moe_dispatch.block_benchmark import capture_forward
+
+        graph = capture_forward(block, x)
+        graph_us = time_loop(graph.replay, args.steps, max(args.warmup, 1))
     counts = block.workspace(x).transport.counts.cpu().numpy()
     offsets = block.workspace(x).transport.offsets.cpu().numpy()
     n_assign = tokens * topk
@@ -355,6 +362,7 @@ def main(argv=None):
                    "tokens": tokens, "hidden": hidden, "intermediate": inter, "experts": experts,
                    "topk": topk, "alignment": cfg.alignment},
         "median_step_us": round(statistics.median(step_us), 2),
+        "forward_graph_us": round(graph_us, 2) if graph_us is not None else None,
         "stages_us": {k: round(v["mean_us"], 2) for k, v in stages.items()},
         "expert_tflops": round(expert_tflops, 1),
         "expert_mfma_frac": round(expert_tflops / BF16_PEAK_TFLOPS, 4),
