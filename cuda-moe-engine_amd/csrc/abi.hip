@@ -13,7 +13,8 @@ namespace moe {
 int launch_topk_route(const float*, const float*, int32_t*, int64_t*, float*, int64_t, int, int,
                       hipStream_t);
 int launch_router_fused(const uint16_t*, const float*, const float*, int32_t*, int64_t*, float*,
-                        float*, int64_t, int, int, int, hipStream_t);
+                        float*, uint16_t*, int64_t, int, int, int, hipStream_t);
+int64_t router_scratch_bytes(int64_t, int64_t);
 int64_t dispatch_scratch_bytes(int64_t, int64_t, int64_t);
 int launch_dispatch(const void*, int, const int32_t*, int32_t*, int32_t*, int32_t*, void*,
                     int32_t*, int32_t*, int64_t, int64_t, int, int, int, bool, hipStream_t);
@@ -93,9 +94,15 @@ int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64
                              static_cast<hipStream_t>(stream));
 }
 
+int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden) {
+    if (experts < 1 || experts > kMaxExperts || hidden < 8 || hidden % 8 != 0) return -1;
+    return router_scratch_bytes(experts, hidden);
+}
+
 int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
-                     int64_t* ids64, float* weights, float* logits_out, int64_t tokens,
-                     int64_t hidden, int64_t experts, int64_t topk, void* stream) {
+                     int64_t* ids64, float* weights, float* logits_out, void* scratch,
+                     int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                     int64_t topk, void* stream) {
     MOE_REQUIRE(tokens >= 0, MOE_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
     MOE_REQUIRE(hidden >= 8 && hidden % 8 == 0 && hidden <= INT_MAX, MOE_ERR_UNSUPPORTED,
                 "fused router needs hidden a positive multiple of 8");
@@ -107,9 +114,14 @@ int moe_router_fused(const void* x, const float* router_w, const float* bias, in
     if (tokens == 0) return MOE_OK;
     MOE_REQUIRE(x && router_w && bias && ids32 && weights, MOE_ERR_INVALID_ARGUMENT,
                 "null pointer");
+    const int64_t need = router_scratch_bytes(experts, hidden);
+    MOE_REQUIRE(scratch && scratch_bytes >= need, MOE_ERR_WORKSPACE,
+                "router scratch needs %lld bytes, got %lld", (long long)need, (long long)scratch_bytes);
+    MOE_REQUIRE(reinterpret_cast<uintptr_t>(scratch) % 16 == 0 && reinterpret_cast<uintptr_t>(router_w) % 16 == 0,
+                MOE_ERR_INVALID_ARGUMENT, "router weights and scratch must be 16-byte aligned");
     return launch_router_fused(static_cast<const uint16_t*>(x), router_w, bias, ids32, ids64,
-                               weights, logits_out, tokens, (int)hidden, (int)experts, (int)topk,
-                               static_cast<hipStream_t>(stream));
+                               weights, logits_out, static_cast<uint16_t*>(scratch), tokens,
+                               (int)hidden, (int)experts, (int)topk, static_cast<hipStream_t>(stream));
 }
 
 int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {

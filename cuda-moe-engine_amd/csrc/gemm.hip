@@ -24,6 +24,7 @@
 //  * Every output element is one MFMA chain in ascending k with one fp32
 //    accumulator, whichever path and tile shape computes it.
 #include <type_traits>
+#include <utility>
 
 #include "moe_common.h"
 
@@ -267,10 +268,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 //    it fetches the logical chunk the swizzle maps there. Buffer resources
 //    bound the valid bytes: rows past the expert's span and weight rows past the
 //    expert read as zero with no per-lane predicate.
-//  * LDS is a ring of four stages of 32 k (A 16 KiB + B 16 KiB each). The loads
-//    of k-step kt+3 are issued while k-step kt computes, and the one barrier per
-//    k-step waits only for the stage about to be read (vmcnt leaves the two
-//    younger stages in flight), so global latency hides behind three k-steps.
+//  * LDS is a ring of stages of 32 k (A TM x 64 B + B BNT x 64 B each; four for
+//    a full 256 x 256 tile, five or six for smaller tiles). The loads of k-step
+//    kt+STAGES-1 are issued while k-step kt computes, and the one barrier per
+//    k-step waits only for the stage about to be read (vmcnt leaves the younger
+//    stages in flight), so global latency hides behind STAGES-1 k-steps.
 //  * Rows of 64 bytes hold 4 chunks of 16 bytes; chunk c of row r sits at
 //    physical chunk c ^ ((r >> 2) & 3), so 16 lanes reading 16 consecutive rows
 //    at one chunk touch all 64 banks once (conflict free).
@@ -284,11 +286,16 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 // ---------------------------------------------------------------------------
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format
 constexpr int kRingK = 32;                     // k per LDS stage
-constexpr int kRingStages = 4;
 constexpr int kRingThreads = 256;
-constexpr uint32_t kRingAStage = 256 * kRingK * 2;            // bytes of one A (or B) stage
-constexpr uint32_t kRingBBase = kRingStages * kRingAStage;    // B stages follow the A stages
-constexpr uint32_t kRingBytes = 2 * kRingStages * kRingAStage;  // 128 KiB
+constexpr uint32_t kRingBytes = 128 * 1024;
+// Stages that fit for a tile of TM activation rows and BNT weight rows (k = 32
+// per stage, 64 bytes per row), at most 6: 4 for full 256 x 256 tiles, 5 or 6
+// for the short row tiles and tail pieces, which do less MFMA work per stage
+// and so need more loads in flight to cover the same latency.
+constexpr int ring_stages(int tm, int bnt) {
+    const int fit = static_cast<int>(kRingBytes / ((tm + bnt) * kRingK * 2));
+    return fit < 6 ? fit : 6;
+}
 
 // Resource descriptor from wave-uniform values, pinned to SGPRs with readfirstlane
 // so buffer instructions take it directly (no waterfall loop).
@@ -322,6 +329,16 @@ __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "m
 
 __device__ __forceinline__ int ring_key(int row) { return (row >> 2) & 3; }
 
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), unrolled.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // silu(g) * u for the fused epilogue: hardware exp2 and reciprocal
 // (v_exp_f32, v_rcp_f32; about 1 ulp each), g and u already rounded to bf16.
 __device__ __forceinline__ float swiglu_fast(float g, float u) {
@@ -343,6 +360,18 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     constexpr int B_LOADS = BNT / 16 / WAVES;
     constexpr int LOADS = A_LOADS + B_LOADS;
     constexpr int H0 = LOADS / 2, H1 = LOADS - H0;
+    constexpr uint32_t A_STAGE = TM * kRingK * 2;   // bytes of one stage of A
+    constexpr uint32_t B_STAGE = BNT * kRingK * 2;  // bytes of one stage of B
+    constexpr int STAGES = ring_stages(TM, BNT);
+    constexpr int AHEAD = STAGES - 1;               // k-step kt+AHEAD loads during kt
+    constexpr uint32_t B_BASE = STAGES * A_STAGE;   // B stages follow the A stages
+    constexpr int SPLIT = 3;                        // stages >= 3 are addressed from second bases
+    static_assert(STAGES >= 4 && STAGES * (A_STAGE + B_STAGE) <= kRingBytes, "ring does not fit");
+    static_assert((SMT - 1) * 2048 + (SPLIT - 1) * A_STAGE < 65536 &&
+                  (SMT - 1) * 2048 + (STAGES - 1 - SPLIT) * A_STAGE < 65536 &&
+                  (SN - 1) * 2048 + (SPLIT - 1) * B_STAGE < 65536 &&
+                  (SN - 1) * 2048 + (STAGES - 1 - SPLIT) * B_STAGE < 65536,
+                  "LDS offsets must fit the 16-bit instruction offset");
     constexpr int NR = SMT + SN;      // fragment reads per k16 slice
     constexpr int NM = SMT * SN;      // MFMAs per k16 slice
     constexpr int kMin = SMT < SN ? SMT : SN;
@@ -391,31 +420,29 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         for (int i = 0; i < LOADS; ++i) {
             if (i < first || i >= first + count) continue;
             if (i < A_LOADS)
-                dma16(rsrc_a, lds + st * kRingAStage + (wave * A_LOADS + i) * 1024, a_off[i], koff);
+                dma16(rsrc_a, lds + st * A_STAGE + (wave * A_LOADS + i) * 1024, a_off[i], koff);
             else
-                dma16(rsrc_b, lds + kRingBBase + st * kRingAStage + (wave * B_LOADS + (i - A_LOADS)) * 1024,
+                dma16(rsrc_b, lds + B_BASE + st * B_STAGE + (wave * B_LOADS + (i - A_LOADS)) * 1024,
                       b_off[i - A_LOADS], koff);
         }
     };
 
-    // Fragment byte addresses in stage 0 for the two k16 slices of a stage; a
-    // stage switch adds a constant offset.
+    // Per-lane fragment byte addresses for the two k16 slices of a stage. The
+    // fragments of sub-tiles i (rows +32 i) share the swizzle key, so sub-tile
+    // and stage only add constants (instruction offsets); stages from SPLIT on
+    // use second bases to keep those offsets below 64 KiB.
     const int frag_row = lane & 31;
     const int frag_half = lane >> 5;
-    uint32_t ra[2][SMT], rb[2][SN];
+    uint32_t va[2], vb[2], va_hi[2], vb_hi[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
         const int chunk = kk * 2 + frag_half;
-#pragma unroll
-        for (int i = 0; i < SMT; ++i) {
-            const int r = wm * WTM + i * 32 + frag_row;
-            ra[kk][i] = static_cast<uint32_t>((r * kRingK + ((chunk ^ ring_key(r)) << 3)) * 2);
-        }
-#pragma unroll
-        for (int j = 0; j < SN; ++j) {
-            const int r = wn * WTN + j * 32 + frag_row;
-            rb[kk][j] = kRingBBase + static_cast<uint32_t>((r * kRingK + ((chunk ^ ring_key(r)) << 3)) * 2);
-        }
+        const int ar = wm * WTM + frag_row;
+        const int br = wn * WTN + frag_row;
+        va[kk] = static_cast<uint32_t>((ar * kRingK + ((chunk ^ ring_key(ar)) << 3)) * 2);
+        vb[kk] = B_BASE + static_cast<uint32_t>((br * kRingK + ((chunk ^ ring_key(br)) << 3)) * 2);
+        va_hi[kk] = va[kk] + SPLIT * A_STAGE;
+        vb_hi[kk] = vb[kk] + SPLIT * B_STAGE;
     }
 
     floatx16 acc[SMT][SN];
@@ -430,10 +457,15 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     auto slot_is_a = [](int r) { return r < 2 * kMin ? (r % 2 == 0) : (SMT > SN); };
     auto slot_index = [](int r) { return r < 2 * kMin ? r / 2 : (r - 2 * kMin) + kMin; };
     auto read_slot = [&](auto st_c, int kk, int r, bf16x8_t (&fa)[SMT], bf16x8_t (&fb)[SN]) {
-        constexpr uint32_t kOff = decltype(st_c)::value * kRingAStage;
+        constexpr int ST = decltype(st_c)::value;
         const int idx = slot_index(r);
-        if (slot_is_a(r)) fa[idx] = *reinterpret_cast<const bf16x8_t*>(lds + ra[kk][idx] + kOff);
-        else fb[idx] = *reinterpret_cast<const bf16x8_t*>(lds + rb[kk][idx] + kOff);
+        if (slot_is_a(r)) {
+            if (ST < SPLIT) fa[idx] = *reinterpret_cast<const bf16x8_t*>(lds + va[kk] + (idx * 2048 + ST * A_STAGE));
+            else fa[idx] = *reinterpret_cast<const bf16x8_t*>(lds + va_hi[kk] + (idx * 2048 + (ST - SPLIT) * A_STAGE));
+        } else {
+            if (ST < SPLIT) fb[idx] = *reinterpret_cast<const bf16x8_t*>(lds + vb[kk] + (idx * 2048 + ST * B_STAGE));
+            else fb[idx] = *reinterpret_cast<const bf16x8_t*>(lds + vb_hi[kk] + (idx * 2048 + (ST - SPLIT) * B_STAGE));
+        }
     };
     // MFMA order within a slice: by the later read slot of its two fragments.
     struct Order { int i[NM]; int j[NM]; };
@@ -472,45 +504,37 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     };
     const int k_steps = static_cast<int>(K / kRingK);
     // k-step kt in stage ST (slice 0 already in fa0/fb0). Its loads of k-step
-    // kt+3 go to stage (ST+3)%4, whose reads all ended before the previous barrier.
+    // kt+AHEAD go to stage (ST+AHEAD)%STAGES, whose reads all ended before the
+    // previous barrier.
     auto step = [&](int kt, auto st_c) {
         constexpr int ST = decltype(st_c)::value;
-        using NX = std::integral_constant<int, (ST + 1) % kRingStages>;
-        const int ahead = min(kt + 3, k_steps - 1);
-        constexpr int LST = (ST + 3) % kRingStages;
+        using NX = std::integral_constant<int, (ST + 1) % STAGES>;
+        const int ahead = min(kt + AHEAD, k_steps - 1);
+        constexpr int LST = (ST + AHEAD) % STAGES;
         fence();
         slice(fa0, fb0, fa1, fb1, st_c, 1, ahead, LST, 0, H0);
-        // k-step kt+1 has landed once at most k-step kt+2's loads and this
-        // step's first part are younger.
-        wait_vm_lgkm0<LOADS + H0>();
+        // k-step kt+1 has landed once at most the loads of k-steps kt+2 ..
+        // kt+AHEAD-1 and this step's first part are younger.
+        wait_vm_lgkm0<(AHEAD - 2) * LOADS + H0>();
         ring_barrier();
         fence();
         slice(fa1, fb1, fa0, fb0, NX{}, 0, ahead, LST, H0, H1);
     };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    using S3 = std::integral_constant<int, 3>;
     // Surplus loads past the last k-step repeat it (same bytes, unread stage),
     // which keeps the per-step load count and the vmcnt bound uniform.
-    issue(0, 0, 0, LOADS);
-    issue(min(1, k_steps - 1), 1, 0, LOADS);
-    issue(min(2, k_steps - 1), 2, 0, LOADS);
-    wait_vm_lgkm0<2 * LOADS>();
+#pragma unroll
+    for (int st = 0; st < AHEAD; ++st) issue(min(st, k_steps - 1), st, 0, LOADS);
+    wait_vm_lgkm0<(AHEAD - 1) * LOADS>();
     ring_barrier();
     fence();
 #pragma unroll
-    for (int r = 0; r < NR; ++r) read_slot(S0{}, 0, r, fa0, fb0);
+    for (int r = 0; r < NR; ++r) read_slot(std::integral_constant<int, 0>{}, 0, r, fa0, fb0);
     int kt = 0;
-    for (; kt + 3 < k_steps; kt += 4) {
-        step(kt, S0{});
-        step(kt + 1, S1{});
-        step(kt + 2, S2{});
-        step(kt + 3, S3{});
-    }
-    if (kt < k_steps) step(kt, S0{});
-    if (kt + 1 < k_steps) step(kt + 1, S1{});
-    if (kt + 2 < k_steps) step(kt + 2, S2{});
+    for (; kt + STAGES - 1 < k_steps; kt += STAGES)
+        static_for<STAGES>([&](auto s_c) { step(kt + decltype(s_c)::value, s_c); });
+    static_for<STAGES - 1>([&](auto s_c) {
+        if (kt + decltype(s_c)::value < k_steps) step(kt + decltype(s_c)::value, s_c);
+    });
     wait_vm_lgkm0<0>();
 
     // Epilogue: one row per lane, four consecutive columns per 8-byte store.

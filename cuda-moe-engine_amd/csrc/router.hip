@@ -104,105 +104,134 @@ __global__ __launch_bounds__(256) void topk_route_kernel(const float* __restrict
 
 // ---------------------------------------------------------------------------
 // Fused router on MFMA. logits = x . W^T with x bf16 and W fp32: W is split
-// exactly-to-24-bits into three bf16 parts (hi = bf16(W), mid = bf16(W - hi),
-// lo = bf16(W - hi - mid)), so x . W = x . hi + x . mid + x . lo with exact
-// bf16 x bf16 products accumulated in fp32 by v_mfma_f32_16x16x32_bf16.
-// A block (4 wavefronts) owns 16 tokens; the waves split the hidden dimension
-// in interleaved 32-wide slices, their partial logits are added in a fixed
-// order through LDS, then each wave runs the top-k of 4 tokens with one lane
-// per expert. Reading x once is the only HBM traffic of consequence.
+// exactly into three bf16 parts (hi = bf16(W), mid = bf16(W - hi),
+// lo = bf16(W - hi - mid); 3 x 8 significant bits cover fp32's 24), so
+// x . W = x . hi + x . mid + x . lo with exact bf16 x bf16 products
+// accumulated in fp32 by v_mfma_f32_16x16x32_bf16.
+//  * router_split_kernel writes the three planes once per call into the
+//    caller's scratch ([3][E][H] bf16), so the VALU split is not repeated by
+//    every token block.
+//  * router_fused_kernel: a block (4 wavefronts) owns 16 tokens; the waves
+//    split the hidden dimension in interleaved 32-wide slices, their partial
+//    logits are added in a fixed order through LDS, then each wave runs the
+//    top-k of 4 tokens with one lane per expert.
 // ---------------------------------------------------------------------------
 typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float rfloatx4_t __attribute__((ext_vector_type(4)));
 constexpr int kRouterTokens = 16;
 
-__device__ __forceinline__ void split3(const float (&w)[8], rbf16x8_t& hi, rbf16x8_t& mid, rbf16x8_t& lo) {
+__global__ __launch_bounds__(256) void router_split_kernel(const float* __restrict__ w,
+                                                           uint16_t* __restrict__ planes, int64_t n) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+    if (i >= n) return;
+    const float4 w0 = *reinterpret_cast<const float4*>(w + i);
+    const float4 w1 = *reinterpret_cast<const float4*>(w + i + 4);
+    const float v[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    uint32_t hi[4], mid[4], lo[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float h = round_bf16(w[j]);
-        const float r1 = w[j] - h;  // exact
-        const float m = round_bf16(r1);
-        const float r2 = r1 - m;    // exact
-        hi[j] = static_cast<__bf16>(h);
-        mid[j] = static_cast<__bf16>(m);
-        lo[j] = static_cast<__bf16>(r2);
+    for (int j = 0; j < 8; j += 2) {
+        float h[2], m[2], l[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            h[t] = round_bf16(v[j + t]);
+            const float r1 = v[j + t] - h[t];  // exact
+            m[t] = round_bf16(r1);
+            l[t] = r1 - m[t];                  // exact, fits bf16
+        }
+        hi[j / 2] = pack_bf16x2(h[0], h[1]);
+        mid[j / 2] = pack_bf16x2(m[0], m[1]);
+        lo[j / 2] = pack_bf16x2(l[0], l[1]);
     }
+    *reinterpret_cast<uint4*>(planes + i) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *reinterpret_cast<uint4*>(planes + n + i) = make_uint4(mid[0], mid[1], mid[2], mid[3]);
+    *reinterpret_cast<uint4*>(planes + 2 * n + i) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
 }
 
-template <int NT>  // expert column tiles of 16: E <= 16 * NT
+// NT expert column tiles of 16 (E <= 16 * NT); MT token tiles of 16 per block,
+// which share each weight slice a block reads from L2.
+template <int NT, int MT>
 __global__ __launch_bounds__(256) void router_fused_kernel(
-    const uint16_t* __restrict__ x, const float* __restrict__ router_w,
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ planes,
     const float* __restrict__ bias, int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
     float* __restrict__ weights, float* __restrict__ logits_out, int64_t tokens, int hidden,
     int experts, int topk) {
-    __shared__ float part[4][kRouterTokens][16 * NT];
+    constexpr int TB = kRouterTokens * MT;  // tokens per block
+    __shared__ float part[4][TB][16 * NT];
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRouterTokens;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TB;
     const int m = lane & 15;   // A row (token) and B column (expert within a tile)
     const int kq = lane >> 4;  // 8-element k block within the 32-wide slice
-    const bool live = t0 + m < tokens;
-    const uint16_t* xrow = x + (live ? t0 + m : t0) * static_cast<int64_t>(hidden);
-
-    rfloatx4_t acc[NT];
+    const int64_t plane = static_cast<int64_t>(experts) * hidden;
+    const uint16_t* xrow[MT];
+    bool live[MT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[nt] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) {
+        const int64_t t = t0 + mt * kRouterTokens + m;
+        live[mt] = t < tokens;
+        xrow[mt] = x + (live[mt] ? t : 0) * static_cast<int64_t>(hidden);
+    }
+
+    rfloatx4_t acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
 
     // Slices are visited in batches of kBatch with every load of a batch issued
     // before its MFMAs, so each wave keeps several 16-byte loads in flight.
-    constexpr int kBatch = 8;
+    constexpr int kBatch = NT * MT >= 8 ? 2 : (NT * MT >= 4 ? 4 : 8);
+    auto load8 = [](const uint16_t* src) {
+        rbf16x8_t v;
+        const uint4 raw = *reinterpret_cast<const uint4*>(src);
+        __builtin_memcpy(&v, &raw, 16);
+        return v;
+    };
+    rbf16x8_t zero;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) zero[j] = static_cast<__bf16>(0.0f);
     for (int kb = wave * 32; kb < hidden; kb += 128 * kBatch) {
-        rbf16x8_t a[kBatch];
-        float w[kBatch][NT][8];
+        rbf16x8_t a[kBatch][MT];
+        rbf16x8_t w[kBatch][NT][3];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int k = kb + u * 128 + kq * 8;
             const bool kin = k < hidden;  // hidden % 8 == 0: a block is all in or all out
-            if (live && kin) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(xrow + k);
-                __builtin_memcpy(&a[u], &raw, 16);
-            } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) a[u][j] = static_cast<__bf16>(0.0f);
-            }
+            for (int mt = 0; mt < MT; ++mt) a[u][mt] = (live[mt] && kin) ? load8(xrow[mt] + k) : zero;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int e = nt * 16 + m;
-                if (e < experts && kin) {
-                    const float* src = router_w + static_cast<int64_t>(e) * hidden + k;
-                    const float4 w0 = *reinterpret_cast<const float4*>(src);
-                    const float4 w1 = *reinterpret_cast<const float4*>(src + 4);
-                    w[u][nt][0] = w0.x; w[u][nt][1] = w0.y; w[u][nt][2] = w0.z; w[u][nt][3] = w0.w;
-                    w[u][nt][4] = w1.x; w[u][nt][5] = w1.y; w[u][nt][6] = w1.z; w[u][nt][7] = w1.w;
-                } else {
+                const bool ok = e < experts && kin;
+                const uint16_t* src = planes + static_cast<int64_t>(e) * hidden + k;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) w[u][nt][j] = 0.0f;
+                for (int q = 0; q < 3; ++q) w[u][nt][q] = ok ? load8(src + q * plane) : zero;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u][mt], w[u][nt][2], acc[mt][nt], 0, 0, 0);
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u][mt], w[u][nt][1], acc[mt][nt], 0, 0, 0);
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u][mt], w[u][nt][0], acc[mt][nt], 0, 0, 0);
                 }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                rbf16x8_t hi, mid, lo;
-                split3(w[u][nt], hi, mid, lo);
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], lo, acc[nt], 0, 0, 0);
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], mid, acc[nt], 0, 0, 0);
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], hi, acc[nt], 0, 0, 0);
-            }
-        }
     }
-    // 16x16 result: lane l holds tokens 4*(l/16) + r, expert column l%16.
+    // 16x16 result: lane l holds tokens 4*(l/16) + r of its token tile, expert column l%16.
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part[wave][4 * kq + r][nt * 16 + m] = acc[nt][r];
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[wave][mt * kRouterTokens + 4 * kq + r][nt * 16 + m] = acc[mt][nt][r];
     __syncthreads();
 
-    // Top-k: wave w handles tokens 4w..4w+3, one lane per expert.
-    for (int i = 0; i < kRouterTokens / 4; ++i) {
-        const int tl = wave * 4 + i;
+    // Top-k: wave w handles tokens w*TB/4 .. (w+1)*TB/4 - 1, one lane per expert.
+    for (int i = 0; i < TB / 4; ++i) {
+        const int tl = wave * (TB / 4) + i;
         const int64_t token = t0 + tl;
         if (token >= tokens) break;
         float v = -INFINITY;
@@ -276,21 +305,31 @@ int launch_topk_route(const float* logits, const float* bias, int32_t* ids32, in
     return check_launch("topk_route_kernel");
 }
 
+int64_t router_scratch_bytes(int64_t experts, int64_t hidden) { return 3 * experts * hidden * 2; }
+
 int launch_router_fused(const uint16_t* x, const float* router_w, const float* bias,
                         int32_t* ids32, int64_t* ids64, float* weights, float* logits_out,
-                        int64_t tokens, int hidden, int experts, int topk, hipStream_t stream) {
+                        uint16_t* planes, int64_t tokens, int hidden, int experts, int topk,
+                        hipStream_t stream) {
     if (tokens == 0) return MOE_OK;
-    const dim3 grid(static_cast<unsigned>((tokens + kRouterTokens - 1) / kRouterTokens));
-#define MOE_ROUTER_CASE(NTV)                                                               \
-    hipLaunchKernelGGL(router_fused_kernel<NTV>, grid, dim3(256), 0, stream, x, router_w,  \
-                       bias, ids32, ids64, weights, logits_out, tokens, hidden, experts,   \
-                       topk)
+    const int64_t n = static_cast<int64_t>(experts) * hidden;
+    hipLaunchKernelGGL(router_split_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0,
+                       stream, router_w, planes, n);
+    const int rc = check_launch("router_split_kernel");
+    if (rc != MOE_OK) return rc;
+    // One token tile per block: measured at E=64, H=2048, T=8192, four tiles per
+    // block (fewer, longer blocks) ran 1.5x slower than one.
+#define MOE_ROUTER_CASE(NTV, MTV)                                                                      \
+    hipLaunchKernelGGL((router_fused_kernel<NTV, MTV>),                                                \
+                       dim3(static_cast<unsigned>((tokens + kRouterTokens * MTV - 1) / (kRouterTokens * MTV))), \
+                       dim3(256), 0, stream, x, planes, bias, ids32, ids64, weights, logits_out, tokens, \
+                       hidden, experts, topk)
     if (experts <= 16) {
-        MOE_ROUTER_CASE(1);
+        MOE_ROUTER_CASE(1, 1);
     } else if (experts <= 32) {
-        MOE_ROUTER_CASE(2);
+        MOE_ROUTER_CASE(2, 1);
     } else if (experts <= 64) {
-        MOE_ROUTER_CASE(4);
+        MOE_ROUTER_CASE(4, 1);
     } else {
         return fail(MOE_ERR_UNSUPPORTED, "experts=%d exceeds 64", experts);
     }

@@ -75,8 +75,16 @@ class HipExtension:
             tokens, experts, topk, _stream(logits.device))
         self.lib.check(status, "topk_route_out")
 
-    def router_fused_out(self, x, router_weight, bias, ids32, ids64, weights, logits=None):
-        """Fused fp32 router projection + top-k (replaces ``layer.py:123,134``)."""
+    def router_scratch_bytes(self, experts, hidden):
+        return int(self.lib.moe_router_scratch_bytes(experts, hidden))
+
+    def router_fused_out(self, x, router_weight, bias, ids32, ids64, weights, logits=None, scratch=None):
+        """Fused fp32 router projection + top-k (replaces ``layer.py:123,134``).
+
+        ``scratch`` (uint8, at least ``router_scratch_bytes(E, H)`` bytes, on the
+        device) receives the bf16 split of the router weights; when omitted a
+        buffer is allocated for this call.
+        """
         _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,
                "expected BF16 GPU x[T,H]")
         tokens, hidden = x.shape
@@ -99,9 +107,14 @@ class HipExtension:
             _check_gpu_tensor(logits, x, "logits")
             _check(logits.shape == (tokens, experts) and logits.dtype == torch.float32,
                    "expected FP32 logits[T,E]")
+        need = self.router_scratch_bytes(experts, hidden)
+        if scratch is None:
+            scratch = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        _check_gpu_tensor(scratch, x, "scratch")
         status = self.lib.moe_router_fused(
             _ptr(x), _ptr(router_weight), _ptr(bias), _ptr(ids32), _ptr(ids64), _ptr(weights),
-            _ptr(logits), tokens, hidden, experts, topk, _stream(x.device))
+            _ptr(logits), _ptr(scratch), scratch.numel() * scratch.element_size(), tokens, hidden,
+            experts, topk, _stream(x.device))
         self.lib.check(status, "router_fused_out")
 
     # -- transport -----------------------------------------------------------

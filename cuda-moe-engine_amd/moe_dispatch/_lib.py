@@ -13,7 +13,7 @@ from functools import lru_cache
 from pathlib import Path
 
 LIBRARY_NAME = "libmoe_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -29,7 +29,8 @@ _SIGNATURES = {
     "moe_status_string": (ctypes.c_char_p, [_int]),
     "moe_last_error": (ctypes.c_char_p, []),
     "moe_topk_route": (_int, [_c_void_p] * 5 + [_i64, _i64, _i64, _c_void_p]),
-    "moe_router_fused": (_int, [_c_void_p] * 7 + [_i64, _i64, _i64, _i64, _c_void_p]),
+    "moe_router_scratch_bytes": (_i64, [_i64, _i64]),
+    "moe_router_fused": (_int, [_c_void_p] * 8 + [_i64] * 5 + [_c_void_p]),
     "moe_dispatch_scratch_bytes": (_i64, [_i64, _i64, _i64]),
     "moe_dispatch": (
         _int,

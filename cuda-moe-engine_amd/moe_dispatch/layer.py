@@ -126,6 +126,7 @@ class MoEBlock(torch.nn.Module):
         self.register_buffer("routing_bias", torch.zeros(cfg.experts, device=device))
         self._workspaces = {}
         self._route_buffers = {}
+        self._router_scratch = None  # bf16 split of the router weights (fused router)
         self._extension = get_extension() if implementation != "torch" else None
 
     def set_routing_pattern(self, pattern):
@@ -153,8 +154,12 @@ class MoEBlock(torch.nn.Module):
                     torch.empty(shape, device=x.device, dtype=torch.float32),
                 )
             ids32, ids64, weights = self._route_buffers[key]
+            if self._router_scratch is None or self._router_scratch.device != x.device:
+                need = self._extension.router_scratch_bytes(self.config.experts, self.config.hidden)
+                self._router_scratch = torch.empty(need, dtype=torch.uint8, device=x.device)
             self._extension.router_fused_out(
-                x, self.router_weight, self.routing_bias, ids32, ids64, weights
+                x, self.router_weight, self.routing_bias, ids32, ids64, weights,
+                scratch=self._router_scratch,
             )
             return ids32, ids64, weights
         logits = torch.nn.functional.linear(x.float(), self.router_weight) + self.routing_bias

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 1
+#define MOE_ABI_VERSION 2
 
 typedef enum {
     MOE_DTYPE_F32 = 0,
@@ -73,15 +73,22 @@ const char* moe_last_error(void);
 int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64_t* ids64,
                    float* weights, int64_t tokens, int64_t experts, int64_t topk, void* stream);
 
+/* Bytes of scratch moe_router_fused needs for (E, H): the bf16 split of router_w. */
+int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden);
+
 /*
  * Fused router: logits = float(x) . router_w^T in fp32, then moe_topk_route's
  * selection. Replaces the F.linear + topk_route_out pair of MoEBlock.route
  * (reference src/moe_dispatch/layer.py:122-135). x is bf16 [T,H]. logits_out
  * ([T,E] fp32) is optional (NULL to skip). ids64 may be NULL.
+ * router_w is split exactly into three bf16 planes (hi, mid, lo) in scratch
+ * (moe_router_scratch_bytes bytes, 16-byte aligned) once per call; the
+ * products x * part are exact and accumulate in fp32 on MFMA.
  */
 int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
-                     int64_t* ids64, float* weights, float* logits_out, int64_t tokens,
-                     int64_t hidden, int64_t experts, int64_t topk, void* stream);
+                     int64_t* ids64, float* weights, float* logits_out, void* scratch,
+                     int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                     int64_t topk, void* stream);
 
 /* Bytes of scratch moe_dispatch needs for (T, E, K). */
 int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk);

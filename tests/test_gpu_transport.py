@@ -136,3 +136,14 @@ def test_standalone_swiglu_and_unused_rows(ext, dtype):
     tol = {torch.bfloat16: 2e-2, torch.float16: 2e-3, torch.float32: 2e-5}[dtype]
     torch.testing.assert_close(output[:21], torch_ref[:21], rtol=tol, atol=tol)
     assert np.all(to_np(output)[21:] == 0)
+
+
+def test_reference_runtime_validation_suite(ext):
+    """The reference's 36-check runtime suite (validation.py:64-104): FP32/FP16,
+    K=1/2, empty batch, empty experts, skew, odd H, scalar and vector paths, plus
+    the PyTorch transport variant."""
+    from moe_dispatch.validation import run_tests
+
+    summary = run_tests(ext)
+    assert summary["passed"] == 36 and summary["failed"] == 0
+    assert summary["max_absolute_error"] < 2e-3
