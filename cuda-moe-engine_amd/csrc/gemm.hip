@@ -1,4 +1,4 @@
-// Grouped bf16 expert GEMMs on CDNA4 MFMA (v_mfma_f32_32x32x16_bf16).
+// Grouped bf16 expert GEMMs on CDNA4 MFMA (v_mfma_f32_16x16x32_bf16; 32x32x16 on the generic path).
 //
 // Problem: for every expert e, rows r in [offsets[e], offsets[e+1]) of A
 // [R, K] multiply B[e]^T (B is [E, N, K], K-contiguous like A) into C [R, N].
@@ -11,9 +11,9 @@
 //
 // Design (gfx950):
 //  * Fast path (K % 32 == 0, the block's shapes): ring_tile / grouped_gemm_ring_kernel
-//    below -- 256 x 256 tiles on four wavefronts of 128 x 128, direct-to-LDS
-//    buffer loads into a four-stage LDS ring, loads three k-steps ahead, MFMAs
-//    interleaved with fragment reads and loads, XCD-aware two-phase tile order.
+//    below -- 256 x 256 tiles on four wavefronts of 128 x 128 (16x16x32 MFMAs),
+//    direct-to-LDS buffer loads into a four-stage LDS ring, loads three k-steps
+//    ahead, MFMAs interleaved with fragment reads, XCD-aware two-phase order.
 //  * Generic path (any K % 8 == 0): grouped_gemm_kernel -- global -> register ->
 //    LDS double buffering with one barrier per 64-wide k-step; LDS rows are 128
 //    bytes with 16-byte chunks XOR-swizzled per row (swz).
@@ -32,6 +32,7 @@ namespace moe {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;  // k-step: one 128-byte LDS row
@@ -260,7 +261,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 // ---------------------------------------------------------------------------
 // Fast path (K % 32 == 0): 256 x 256 output tiles computed by four wavefronts
 // (one per SIMD), each owning 128 x 128 (or (TM/2) x (BNT/2) for the short last
-// row tile of an expert and the split tail pieces).
+// row tile of an expert and the split tail pieces) as a grid of 16 x 16 blocks
+// on v_mfma_f32_16x16x32_bf16.
 //
 //  * Operands reach LDS through direct-to-LDS buffer loads
 //    (buffer_load_dwordx4 ... lds): a wavefront load moves 16 rows of 64 bytes
@@ -269,29 +271,25 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 //    bound the valid bytes: rows past the expert's span and weight rows past the
 //    expert read as zero with no per-lane predicate.
 //  * LDS is a ring of stages of 32 k (A TM x 64 B + B BNT x 64 B each; four for
-//    a full 256 x 256 tile, five or six for smaller tiles). The loads of k-step
+//    a full 256 x 256 tile, six for the 64-row tiles). The loads of k-step
 //    kt+STAGES-1 are issued while k-step kt computes, and the one barrier per
 //    k-step waits only for the stage about to be read (vmcnt leaves the younger
 //    stages in flight), so global latency hides behind STAGES-1 k-steps.
 //  * Rows of 64 bytes hold 4 chunks of 16 bytes; chunk c of row r sits at
 //    physical chunk c ^ ((r >> 2) & 3), so 16 lanes reading 16 consecutive rows
 //    at one chunk touch all 64 banks once (conflict free).
-//  * Inside a k16 slice every MFMA is followed by at most one fragment read of
-//    the next slice and by its share of the next loads; fragments are read A
-//    and B alternately and the next slice's MFMAs run in order of the later of
-//    their two fragments, so each read has about a slice of MFMA work to land.
-//    sched_barrier fences pin this order.
-//  * The k order of each output's MFMA chain (ascending k, one accumulator) is
-//    the same as the generic path, whatever the tile shape.
+//  * Fragment reads of the next stage are spread between the MFMAs of the
+//    current one, each well ahead of its use, and a single set of fragment
+//    registers is live (see ring_tile). sched_barrier fences pin the order.
+//  * The k order of each output's MFMA chain (ascending k in groups of 8, one
+//    accumulator) is the same as the generic path, whatever the tile shape.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format
 constexpr int kRingK = 32;                     // k per LDS stage
 constexpr int kRingThreads = 256;
 constexpr uint32_t kRingBytes = 128 * 1024;
 // Stages that fit for a tile of TM activation rows and BNT weight rows (k = 32
-// per stage, 64 bytes per row), at most 6: 4 for full 256 x 256 tiles, 5 or 6
-// for the short row tiles and tail pieces, which do less MFMA work per stage
-// and so need more loads in flight to cover the same latency.
+// per stage, 64 bytes per row), at most 6.
 constexpr int ring_stages(int tm, int bnt) {
     const int fit = static_cast<int>(kRingBytes / ((tm + bnt) * kRingK * 2));
     return fit < 6 ? fit : 6;
@@ -346,8 +344,14 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
     return (g * u) * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// One output tile: rows [row0, row0 + SMT*64) of one expert (clamped to
-// row_end) by BNT weight rows starting at output column col0.
+// One output tile on v_mfma_f32_16x16x32_bf16: rows [row0, row0 + SMT*64) of one
+// expert (clamped to row_end) by BNT weight rows starting at output column
+// col0. A k-step is one 32-k stage: every wave multiplies its (WTM/16) x (WTN/16)
+// grid of 16x16 blocks with one MFMA each while it reads the next stage's
+// fragments and issues loads for a stage AHEAD steps on. The 16x16x32 form
+// sustains a higher clock than 32x32x16 under the power limit (measured on
+// MI355X: 1.91 vs 1.66 GHz with the same read and load mix), so it moves the
+// same FLOPs about 10% faster.
 template <int SMT, int BNT, bool SWIGLU>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end) {
@@ -355,28 +359,20 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     constexpr int TM = SMT * 64;
     constexpr int WTM = TM / 2;
     constexpr int WTN = BNT / 2;
-    constexpr int SN = WTN / 32;
+    constexpr int FA = WTM / 16;       // 16-row A fragments per wave
+    constexpr int FB = WTN / 16;       // 16-row B fragments per wave
     constexpr int A_LOADS = TM / 16 / WAVES;
     constexpr int B_LOADS = BNT / 16 / WAVES;
     constexpr int LOADS = A_LOADS + B_LOADS;
-    constexpr int H0 = LOADS / 2, H1 = LOADS - H0;
     constexpr uint32_t A_STAGE = TM * kRingK * 2;   // bytes of one stage of A
     constexpr uint32_t B_STAGE = BNT * kRingK * 2;  // bytes of one stage of B
-    constexpr int STAGES = ring_stages(TM, BNT);
+    constexpr int STAGES = ring_stages(TM, BNT) >= 6 ? 6 : 4;  // 4 for 256x256 and 256x128 tiles
     constexpr int AHEAD = STAGES - 1;               // k-step kt+AHEAD loads during kt
     constexpr uint32_t B_BASE = STAGES * A_STAGE;   // B stages follow the A stages
-    constexpr int SPLIT = 3;                        // stages >= 3 are addressed from second bases
-    static_assert(STAGES >= 4 && STAGES * (A_STAGE + B_STAGE) <= kRingBytes, "ring does not fit");
-    static_assert((SMT - 1) * 2048 + (SPLIT - 1) * A_STAGE < 65536 &&
-                  (SMT - 1) * 2048 + (STAGES - 1 - SPLIT) * A_STAGE < 65536 &&
-                  (SN - 1) * 2048 + (SPLIT - 1) * B_STAGE < 65536 &&
-                  (SN - 1) * 2048 + (STAGES - 1 - SPLIT) * B_STAGE < 65536,
-                  "LDS offsets must fit the 16-bit instruction offset");
-    constexpr int NR = SMT + SN;      // fragment reads per k16 slice
-    constexpr int NM = SMT * SN;      // MFMAs per k16 slice
-    constexpr int kMin = SMT < SN ? SMT : SN;
-    static_assert(A_LOADS >= 1 && B_LOADS >= 1 && SN >= 1, "tile shape");
-    static_assert(!SWIGLU || SN % 2 == 0, "gate/up pairing needs an even sub-tile count");
+    static_assert(A_LOADS >= 1 && B_LOADS >= 1 && FA >= 1 && FB >= 2, "tile shape");
+    static_assert(!SWIGLU || FB % 2 == 0, "gate/up pairing needs an even fragment count");
+    static_assert(STAGES * (A_STAGE + B_STAGE) <= kRingBytes, "ring does not fit");
+    static_assert((FA - 1) * 1024 < 65536 && (FB - 1) * 1024 < 65536, "fragment offsets fit the instruction offset");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / 2;
@@ -427,153 +423,133 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         }
     };
 
-    // Per-lane fragment byte addresses for the two k16 slices of a stage. The
-    // fragments of sub-tiles i (rows +32 i) share the swizzle key, so sub-tile
-    // and stage only add constants (instruction offsets); stages from SPLIT on
-    // use second bases to keep those offsets below 64 KiB.
-    const int frag_row = lane & 31;
-    const int frag_half = lane >> 5;
-    uint32_t va[2], vb[2], va_hi[2], vb_hi[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-        const int chunk = kk * 2 + frag_half;
-        const int ar = wm * WTM + frag_row;
-        const int br = wn * WTN + frag_row;
-        va[kk] = static_cast<uint32_t>((ar * kRingK + ((chunk ^ ring_key(ar)) << 3)) * 2);
-        vb[kk] = B_BASE + static_cast<uint32_t>((br * kRingK + ((chunk ^ ring_key(br)) << 3)) * 2);
-        va_hi[kk] = va[kk] + SPLIT * A_STAGE;
-        vb_hi[kk] = vb[kk] + SPLIT * B_STAGE;
-    }
+    // Per-lane fragment addresses: lane l reads row (l%16) of a fragment at k
+    // chunk l/16 (all 32 k of the stage in one 16-byte read). Fragments 16 rows
+    // apart share the swizzle key, so fragment and stage only add constants
+    // (instruction offsets); stages from SPLIT on use second bases to keep those
+    // offsets below 64 KiB.
+    const int frag_row = lane & 15;
+    const int chunk = lane >> 4;
+    const int ar = wm * WTM + frag_row;
+    const int br = wn * WTN + frag_row;
+    const uint32_t va = static_cast<uint32_t>((ar * kRingK + ((chunk ^ ring_key(ar)) << 3)) * 2);
+    const uint32_t vb = B_BASE + static_cast<uint32_t>((br * kRingK + ((chunk ^ ring_key(br)) << 3)) * 2);
 
-    floatx16 acc[SMT][SN];
+    floatx4 acc[FA][FB];
 #pragma unroll
-    for (int i = 0; i < SMT; ++i)
+    for (int i = 0; i < FA; ++i)
 #pragma unroll
-        for (int j = 0; j < SN; ++j)
+        for (int j = 0; j < FB; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
 
-    // Read slot r: A and B fragments alternate while both remain.
-    auto slot_is_a = [](int r) { return r < 2 * kMin ? (r % 2 == 0) : (SMT > SN); };
-    auto slot_index = [](int r) { return r < 2 * kMin ? r / 2 : (r - 2 * kMin) + kMin; };
-    auto read_slot = [&](auto st_c, int kk, int r, bf16x8_t (&fa)[SMT], bf16x8_t (&fb)[SN]) {
-        constexpr int ST = decltype(st_c)::value;
-        const int idx = slot_index(r);
-        if (slot_is_a(r)) {
-            if (ST < SPLIT) fa[idx] = *reinterpret_cast<const bf16x8_t*>(lds + va[kk] + (idx * 2048 + ST * A_STAGE));
-            else fa[idx] = *reinterpret_cast<const bf16x8_t*>(lds + va_hi[kk] + (idx * 2048 + (ST - SPLIT) * A_STAGE));
-        } else {
-            if (ST < SPLIT) fb[idx] = *reinterpret_cast<const bf16x8_t*>(lds + vb[kk] + (idx * 2048 + ST * B_STAGE));
-            else fb[idx] = *reinterpret_cast<const bf16x8_t*>(lds + vb_hi[kk] + (idx * 2048 + (ST - SPLIT) * B_STAGE));
-        }
+    // Fragment reads at a stage base (per-lane address of stage st, computed
+    // once per k-step); the fragment index is an instruction offset.
+    auto read_at = [&](uint32_t base, int idx) {
+        return *reinterpret_cast<const bf16x8_t*>(lds + base + idx * 1024);
     };
-    // MFMA order within a slice: by the later read slot of its two fragments.
-    struct Order { int i[NM]; int j[NM]; };
-    constexpr Order order = [] {
-        Order o{};
-        int n = 0;
-        for (int s = 0; s < NR; ++s)
-            for (int i = 0; i < SMT; ++i)
-                for (int j = 0; j < SN; ++j) {
-                    const int ai = i < kMin ? 2 * i : 2 * kMin + (i - kMin);
-                    const int bj = j < kMin ? 2 * j + 1 : 2 * kMin + (j - kMin);
-                    if ((ai > bj ? ai : bj) == s) { o.i[n] = i; o.j[n] = j; ++n; }
-                }
-        return o;
-    }();
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
 
-    // Weights fragment as src0, activations as src1: the 32x32 result comes out
-    // transposed, so lane l holds row l%32 and, in registers 4q..4q+3, the four
-    // consecutive columns 8q + 4*(l/32) + 0..3 (packed 8-byte stores).
-    bf16x8_t fa0[SMT], fb0[SN], fa1[SMT], fb1[SN];
-    auto slice = [&](const bf16x8_t (&ca)[SMT], const bf16x8_t (&cb)[SN], bf16x8_t (&na)[SMT],
-                     bf16x8_t (&nb)[SN], auto rs_c, int rkk, int lkt, int lst, int first, int count) {
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-            acc[order.i[m]][order.j[m]] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                cb[order.j[m]], ca[order.i[m]], acc[order.i[m]][order.j[m]], 0, 0, 0);
-            const int r0 = NR <= NM ? (m < NR ? m : NR) : m * NR / NM;
-            const int r1 = NR <= NM ? (m < NR ? m + 1 : NR) : (m + 1) * NR / NM;
-#pragma unroll
-            for (int r = r0; r < r1; ++r) read_slot(rs_c, rkk, r, na, nb);
-            const int q0 = m * count / NM, q1 = (m + 1) * count / NM;
-            if (q1 > q0) issue(lkt, lst, first + q0, q1 - q0);
-            fence();
-        }
-    };
+    // Weights fragment as src0, activations as src1: the 16x16 result comes out
+    // transposed, so lane l holds row l%16 and the four consecutive columns
+    // 4*(l/16) + 0..3 (packed 8-byte stores).
+    //
+    // One set of fragments (FA A + FB B) is live. A k-step runs in two halves:
+    // B fragments [0, FB/2) with every A fragment, then [FB/2, FB). During the
+    // first half this stage's B fragments [FB/2, FB) are read (their previous
+    // values were last used by the previous step's second half); during the
+    // second half the next stage's A fragment i is read right after its last
+    // MFMA, and the next stage's B fragments [0, FB/2). Every read has at least
+    // about a quarter of a k-step of MFMA work before its first use. The k-loop
+    // is not unrolled (stage addresses are computed per step), so each
+    // accumulator keeps one register through the loop.
+    constexpr int HB = FB / 2;
+    constexpr int HM = FA * HB;        // MFMAs per half
+    static_assert(HB >= 1 && HM >= HB, "half-step shape");
+    bf16x8_t fa[FA], fb[FB];
     const int k_steps = static_cast<int>(K / kRingK);
-    // k-step kt in stage ST (slice 0 already in fa0/fb0). Its loads of k-step
-    // kt+AHEAD go to stage (ST+AHEAD)%STAGES, whose reads all ended before the
-    // previous barrier.
-    auto step = [&](int kt, auto st_c) {
-        constexpr int ST = decltype(st_c)::value;
-        using NX = std::integral_constant<int, (ST + 1) % STAGES>;
-        const int ahead = min(kt + AHEAD, k_steps - 1);
-        constexpr int LST = (ST + AHEAD) % STAGES;
-        fence();
-        slice(fa0, fb0, fa1, fb1, st_c, 1, ahead, LST, 0, H0);
-        // k-step kt+1 has landed once at most the loads of k-steps kt+2 ..
-        // kt+AHEAD-1 and this step's first part are younger.
-        wait_vm_lgkm0<(AHEAD - 2) * LOADS + H0>();
-        ring_barrier();
-        fence();
-        slice(fa1, fb1, fa0, fb0, NX{}, 0, ahead, LST, H0, H1);
-    };
-    // Surplus loads past the last k-step repeat it (same bytes, unread stage),
-    // which keeps the per-step load count and the vmcnt bound uniform.
+    // Loads go in two blocks per k-step: one load between each pair of MFMAs
+    // makes the register allocator shuffle the accumulators through copies.
 #pragma unroll
     for (int st = 0; st < AHEAD; ++st) issue(min(st, k_steps - 1), st, 0, LOADS);
     wait_vm_lgkm0<(AHEAD - 1) * LOADS>();
     ring_barrier();
     fence();
 #pragma unroll
-    for (int r = 0; r < NR; ++r) read_slot(std::integral_constant<int, 0>{}, 0, r, fa0, fb0);
-    int kt = 0;
-    for (; kt + STAGES - 1 < k_steps; kt += STAGES)
-        static_for<STAGES>([&](auto s_c) { step(kt + decltype(s_c)::value, s_c); });
-    static_for<STAGES - 1>([&](auto s_c) {
-        if (kt + decltype(s_c)::value < k_steps) step(kt + decltype(s_c)::value, s_c);
-    });
+    for (int i = 0; i < FA; ++i) fa[i] = read_at(va, i);
+#pragma unroll
+    for (int j = 0; j < HB; ++j) fb[j] = read_at(vb, j);
+    int st = 0;
+    for (int kt = 0; kt < k_steps; ++kt) {
+        // k-step kt in stage st; its loads (k-step kt+AHEAD) go to stage
+        // (st+AHEAD)%STAGES, whose reads all ended before the previous barrier.
+        const int nx = st + 1 == STAGES ? 0 : st + 1;
+        const int lst = st == 0 ? STAGES - 1 : st - 1;
+        const int ahead = min(kt + AHEAD, k_steps - 1);
+        const uint32_t b_cur = vb + st * B_STAGE;
+        const uint32_t a_nx = va + nx * A_STAGE, b_nx = vb + nx * B_STAGE;
+        fence();
+        // Stage kt+1 has landed once at most k-steps kt+2 .. kt+AHEAD-1 are younger.
+        wait_vm_lgkm0<(AHEAD - 2) * LOADS>();
+        ring_barrier();
+        fence();
+        issue(ahead, lst, 0, LOADS / 2);
+        fence();
+        static_for<HM>([&](auto m_c) {
+            constexpr int m = decltype(m_c)::value;
+            constexpr int i = m / HB, j = m % HB;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+            if constexpr (m % 2 == 0 && m / 2 < HB) fb[HB + m / 2] = read_at(b_cur, HB + m / 2);
+            fence();
+        });
+        issue(ahead, lst, LOADS / 2, LOADS - LOADS / 2);
+        fence();
+        static_for<HM>([&](auto m_c) {
+            constexpr int m = decltype(m_c)::value;
+            constexpr int i = m / HB, j = HB + m % HB;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+            if constexpr (m % 2 == 1 && m / 2 < HB) fb[m / 2] = read_at(b_nx, m / 2);
+            if constexpr (m % HB == HB - 1) fa[i] = read_at(a_nx, i);
+            fence();
+        });
+        st = nx;
+    }
     wait_vm_lgkm0<0>();
 
     // Epilogue: one row per lane, four consecutive columns per 8-byte store.
-    const int col4 = 4 * (lane >> 5);
+    // Each row of accumulators is first moved to VGPRs through an empty asm
+    // operand: without it the register allocator shapes the accumulators' AGPR
+    // assignment after the epilogue's register pairs and copies them inside the
+    // k-loop on every step.
+    const int col4 = 4 * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < SMT; ++i) {
-        const int64_t grow = row0 + wm * WTM + i * 32 + (lane & 31);
+    for (int i = 0; i < FA; ++i) {
+#pragma unroll
+        for (int j = 0; j < FB; ++j) asm volatile("" : "+v"(acc[i][j]));
+        const int64_t grow = row0 + wm * WTM + i * 16 + (lane & 15);
         if (grow >= row_end) continue;
         uint16_t* crow = p.c + grow * p.ldc;
         if constexpr (SWIGLU) {
 #pragma unroll
-            for (int j = 0; j < SN / 2; ++j) {
-                const int64_t cbase = col0 + wn * (WTN / 2) + j * 32 + col4;
+            for (int j = 0; j < FB / 2; ++j) {
+                const int64_t col = col0 + wn * (WTN / 2) + j * 16 + col4;
+                if (col >= p.n_out) continue;
+                float act[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int64_t col = cbase + 8 * q;
-                    if (col >= p.n_out) continue;
-                    float act[4];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const uint32_t gu = pack_bf16x2(acc[i][j][4 * q + t], acc[i][j + SN / 2][4 * q + t]);
-                        act[t] = swiglu_fast(__uint_as_float(gu << 16), __uint_as_float(gu & 0xffff0000u));
-                    }
-                    *reinterpret_cast<uint2*>(crow + col) =
-                        make_uint2(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]));
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t gu = pack_bf16x2(acc[i][j][t], acc[i][j + FB / 2][t]);
+                    act[t] = swiglu_fast(__uint_as_float(gu << 16), __uint_as_float(gu & 0xffff0000u));
                 }
+                *reinterpret_cast<uint2*>(crow + col) =
+                    make_uint2(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]));
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < SN; ++j) {
-                const int64_t cbase = col0 + wn * WTN + j * 32 + col4;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int64_t col = cbase + 8 * q;
-                    if (col >= p.n_out) continue;
-                    *reinterpret_cast<uint2*>(crow + col) =
-                        make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                                   pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
-                }
+            for (int j = 0; j < FB; ++j) {
+                const int64_t col = col0 + wn * WTN + j * 16 + col4;
+                if (col >= p.n_out) continue;
+                *reinterpret_cast<uint2*>(crow + col) =
+                    make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
             }
         }
     }
