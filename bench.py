@@ -186,6 +186,35 @@ def measured_traffic(config, kernels):
     return total
 
 
+def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, launch_us):
+    """Roofline entry for the gate/up GEMM + SwiGLU launch.
+
+    Algorithmic bytes per launch: the weights of the experts that hold rows
+    (2I x H bf16 each), the packed activations read once (rows x H bf16) and the
+    activated output written once (assignments x I bf16). When flop/byte is below
+    the MI355X ridge point (2500 TFLOP/s / 8 TB/s = 312.5) the launch is bound by
+    HBM and the entry is in GB/s; otherwise by the bf16 MFMA peak, in TFLOP/s.
+    Launches of at most 128 packed rows run the 64-column decode kernel.
+    """
+    active = int((counts > 0).sum())
+    byte = 2.0 * (active * 2 * inter * hidden + n_assign * hidden + n_assign * inter)
+    kernel = "grouped_gemm_narrow_kernel<true>" if packed_rows <= 128 else "grouped_gemm_ring_kernel<true>"
+    entry = {"kernel": kernel + " (gate/up GEMM + SwiGLU epilogue)"}
+    if flop / byte < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+        achieved = byte / (launch_us * 1e-6) / 1e9
+        entry.update(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                     frac=round(achieved / HBM_PEAK_GBS, 4))
+    else:
+        achieved = flop / (launch_us * 1e-6) / 1e12
+        entry.update(bound="mfma", achieved=round(achieved, 1), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                     frac=round(achieved / BF16_PEAK_TFLOPS, 4))
+    entry.update(traffic=measured_traffic(config, (kernel,)), flop_per_launch=flop, bytes_per_launch=byte,
+                 avg_launch_us=round(launch_us, 2))
+    # "bound" first, as the contract lists it
+    return {k: entry[k] for k in ("bound", "kernel", "achieved", "peak", "unit", "frac", "traffic",
+                                  "flop_per_launch", "bytes_per_launch", "avg_launch_us")}
+
+
 def copy_calibration(steps):
     """1 GiB device-to-device copy: reads and writes exactly 2^30 bytes per launch."""
     import torch
@@ -342,7 +371,6 @@ def main(argv=None):
     expert_tflops = (gateup_flop + down_flop) / ((t_gu + t_dn) * 1e-6) / 1e12
     disp_bytes = oracle.dispatch_bytes(tokens, hidden, topk, pad_rows)
     comb_bytes = oracle.combine_bytes(tokens, hidden, topk)
-    gu_tflops = gateup_flop / (t_gu * 1e-6) / 1e12
 
     result = {
         "metric": "MoE block fwd latency (us) + expert TFLOP/s % bf16 MFMA peak; dispatch GB/s",
@@ -369,17 +397,8 @@ def main(argv=None):
         "dispatch_gbs": round(disp_bytes / (stages["dispatch"]["mean_us"] * 1e-6) / 1e9, 1),
         "combine_gbs": round(comb_bytes / (stages["combine"]["mean_us"] * 1e-6) / 1e9, 1),
         "expert_counts": counts.tolist(),
-        "roofline": {
-            "bound": "mfma",
-            "kernel": "grouped_gemm_ring_kernel<true> (gate/up GEMM + SwiGLU epilogue)",
-            "achieved": round(gu_tflops, 1),
-            "peak": BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(gu_tflops / BF16_PEAK_TFLOPS, 4),
-            "traffic": measured_traffic(args.config, ("grouped_gemm_ring_kernel<true>",)),
-            "flop_per_launch": gateup_flop,
-            "avg_launch_us": round(t_gu, 2),
-        },
+        "roofline": gateup_roofline(args.config, counts, block.workspace(x).transport.packed.shape[0],
+                                    hidden, inter, n_assign, gateup_flop, t_gu),
     }
     if not args.no_torch_variant:
         try:

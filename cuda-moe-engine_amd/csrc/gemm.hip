@@ -658,6 +658,39 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_ring_kernel(GemmPar
     }
 }
 
+// Decode-sized launches (at most 128 rows in all): every expert has at most one
+// row tile, so the work is streaming the active experts' weights. Tiles are 64
+// output columns wide, four times as many as the 256-wide tiles, so that a
+// single token's two experts still spread over the CUs. Each output is the
+// same MFMA chain in k order as on the wide path. MAX_ROWS (64 or 128) bounds
+// every expert's span; the 64-row instance needs less LDS, so more blocks share
+// a CU.
+constexpr int kNarrowCols = 64;
+
+template <bool SWIGLU, int MAX_ROWS>
+__global__ __launch_bounds__(kRingThreads) void grouped_gemm_narrow_kernel(GemmParams p) {
+    constexpr int BNT = SWIGLU ? 2 * kNarrowCols : kNarrowCols;
+    constexpr uint32_t kLds = 6 * (MAX_ROWS + BNT) * kRingK * 2;  // six stages of the largest tile
+    static_assert(MAX_ROWS == 64 || MAX_ROWS == 128, "narrow row tiles");
+    static_assert(ring_stages(MAX_ROWS, BNT) >= 6 && ring_stages(64, BNT) >= 6, "narrow tiles use six stages");
+    __shared__ __attribute__((aligned(1024))) char lds[kLds];
+    const int expert = blockIdx.x / p.n_tiles;
+    const int n_tile = blockIdx.x - expert * p.n_tiles;
+    if (expert >= p.experts) return;
+    const int64_t row0 = p.offsets[expert];
+    const int64_t row_end = min(static_cast<int64_t>(p.offsets[expert + 1]), p.rows);
+    if (row0 < 0 || row0 >= row_end) return;
+    const int64_t span = row_end - row0;  // <= p.rows <= MAX_ROWS (checked by the launcher)
+    const int64_t col0 = static_cast<int64_t>(n_tile) * kNarrowCols;
+    if constexpr (MAX_ROWS == 128) {
+        if (span > 64) {
+            ring_tile<2, BNT, SWIGLU>(p, lds, expert, col0, row0, row_end);
+            return;
+        }
+    }
+    ring_tile<1, BNT, SWIGLU>(p, lds, expert, col0, row0, row_end);
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
@@ -684,6 +717,19 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     int64_t blocks = m_bound * p.n_tiles;
     if (blocks == 0) return MOE_OK;
     p.n_cu = device_cu_count();
+    if (BM == 256 && BN == 256 && p.k % kRingK == 0 && rows <= 128) {
+        GemmParams q = p;
+        q.n_tiles = static_cast<int>((p.n_out + kNarrowCols - 1) / kNarrowCols);
+        const int64_t narrow_blocks = static_cast<int64_t>(p.experts) * q.n_tiles;
+        if (narrow_blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
+        if (rows <= 64)
+            hipLaunchKernelGGL((grouped_gemm_narrow_kernel<SWIGLU, 64>), dim3(static_cast<unsigned>(narrow_blocks)),
+                               dim3(kRingThreads), 0, stream, q);
+        else
+            hipLaunchKernelGGL((grouped_gemm_narrow_kernel<SWIGLU, 128>), dim3(static_cast<unsigned>(narrow_blocks)),
+                               dim3(kRingThreads), 0, stream, q);
+        return check_launch("grouped_gemm_narrow_kernel");
+    }
     if (BM == 256 && BN == 256 && p.k % kRingK == 0) {
         // Two phases, each rounded up to the XCD count, plus room for the split
         // tail pieces (at most n_cu per phase).

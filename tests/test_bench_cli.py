@@ -40,3 +40,22 @@ def test_committed_traffic_table_covers_the_bench_kernels():
     table = json.loads((ROOT / "profiles" / "hbm_traffic.json").read_text())
     assert "grouped_gemm_ring_kernel<true>" in table["c4_t4096"]
     assert {"count_rank_kernel", "pack_kernel<16>"} <= set(table["c2_transport"])
+
+
+def test_gateup_roofline_picks_the_bound_by_intensity():
+    import numpy as np
+
+    h, i = 4096, 14336
+    # Decode: one token on two experts streams 2 x (2I x H) bf16 weights for 4*2*H*I flop.
+    dec = bench.gateup_roofline("none", np.array([1, 0, 0, 0, 0, 1, 0, 0]), 58, h, i, 2, 4.0 * 2 * h * i, 100.0)
+    weights = 2 * 2 * (2 * i * h)
+    assert dec["bound"] == "hbm" and dec["unit"] == "GB/s" and dec["peak"] == bench.HBM_PEAK_GBS
+    assert dec["kernel"].startswith("grouped_gemm_narrow_kernel<true>")
+    assert weights < dec["bytes_per_launch"] < weights * 1.001
+    assert abs(dec["achieved"] - dec["bytes_per_launch"] / 100e-6 / 1e9) < 0.1
+    # Prefill: 8192 assignments over 8 experts is far past the ridge point.
+    pre = bench.gateup_roofline("none", np.array([1024] * 8), 8248, h, i, 8192, 4.0 * 8192 * h * i, 1000.0)
+    assert pre["bound"] == "mfma" and pre["unit"] == "TFLOP/s"
+    assert pre["kernel"].startswith("grouped_gemm_ring_kernel<true>")
+    assert abs(pre["achieved"] - 4.0 * 8192 * h * i / 1e-3 / 1e12) < 0.1
+    assert list(pre)[0] == "bound"

@@ -5,7 +5,8 @@ fp32 rounding per group): at least 99.99% of the bf16 outputs identical and the
 rest one bf16 step away (see tests/_helpers.assert_near_bit_exact); and,
 independently, within one bf16 rounding of the exact float64 product. Covers empty experts,
 skewed row counts, partial row tiles, short reductions (K < 64), column counts
-that are not multiples of the column tile, and the fused gate/up + SwiGLU
+that are not multiples of the column tile, decode-sized launches (at most 128
+rows, which take 64-column tiles), and the fused gate/up + SwiGLU
 epilogue against the kernels' own unfused pipeline (grouped GEMM -> bf16
 projection -> standalone SwiGLU). The two see the same bf16 gate and up values;
 the fused epilogue evaluates silu with the hardware exp2 and reciprocal
@@ -45,6 +46,9 @@ GEMM_CASES = [
     ([1024, 1030, 998, 1051], 8, 264, 200),
     ([33] * 16, 1, 128, 1024),
     ([2000, 0], 8, 1024, 512),
+    # at most 128 rows in all: the 64-column decode tiles
+    ([90, 20, 0], 8, 200, 96),
+    ([1, 0, 1], 1, 1000, 64),
 ]
 
 
@@ -74,6 +78,9 @@ GATEUP_CASES = [
     ([700, 3, 0, 260], 8, 32, 384),
     ([129, 255, 256, 257], 8, 512, 136),
     ([2000, 17], 8, 1024, 1408),
+    # at most 128 rows in all: the 64-column decode tiles
+    ([70, 9], 8, 96, 200),
+    ([2, 0, 0, 1], 1, 512, 64),
 ]
 
 
