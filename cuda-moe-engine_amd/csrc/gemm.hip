@@ -10,10 +10,11 @@
 // same lane, so the activation is computed in registers.
 //
 // Design (gfx950):
-//  * Fast path (K % 32 == 0, the block's shapes): ring_tile / grouped_gemm_ring_kernel
+//  * Fast path (K % 64 == 0, the block's shapes): ring_tile / grouped_gemm_ring_kernel
 //    below -- 256 x 256 tiles on four wavefronts of 128 x 128 (16x16x32 MFMAs),
-//    direct-to-LDS buffer loads into a four-stage LDS ring, loads three k-steps
-//    ahead, MFMAs interleaved with fragment reads, XCD-aware two-phase order.
+//    direct-to-LDS buffer loads of whole 128-byte lines into an LDS ring of
+//    64-k stages, MFMAs interleaved with fragment reads and loads, XCD-aware
+//    two-phase order; 64-column tiles for decode-sized launches.
 //  * Generic path (any K % 8 == 0): grouped_gemm_kernel -- global -> register ->
 //    LDS double buffering with one barrier per 64-wide k-step; LDS rows are 128
 //    bytes with 16-byte chunks XOR-swizzled per row (swz).
@@ -259,40 +260,55 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 }
 
 // ---------------------------------------------------------------------------
-// Fast path (K % 32 == 0): 256 x 256 output tiles computed by four wavefronts
+// Fast path (K % 64 == 0): 256 x 256 output tiles computed by four wavefronts
 // (one per SIMD), each owning 128 x 128 (or (TM/2) x (BNT/2) for the short last
-// row tile of an expert and the split tail pieces) as a grid of 16 x 16 blocks
-// on v_mfma_f32_16x16x32_bf16.
+// row tile of an expert, the split tail pieces and decode tiles) as a grid of
+// 16 x 16 blocks on v_mfma_f32_16x16x32_bf16.
 //
 //  * Operands reach LDS through direct-to-LDS buffer loads
-//    (buffer_load_dwordx4 ... lds): a wavefront load moves 16 rows of 64 bytes
-//    (1 KiB), lane l landing at byte 16*l, i.e. row l/4, physical chunk l%4, so
-//    it fetches the logical chunk the swizzle maps there. Buffer resources
-//    bound the valid bytes: rows past the expert's span and weight rows past the
+//    (buffer_load_dwordx4 ... lds). One wavefront load moves 8 rows of 128
+//    bytes (64 k), lane l landing at byte 16*l, i.e. row l/8, physical chunk
+//    l%8, so it fetches the logical chunk the swizzle maps there. Each group of
+//    8 lanes covers one whole 128-byte line: the vector L1 sends full-line
+//    requests to L2. With 64-byte (32-k) rows every line took two requests, and
+//    the number of requests a CU keeps in flight capped the load rate (measured:
+//    the gate/up GEMM 9% and the down GEMM 13% slower). Buffer resources bound
+//    the valid bytes: rows past the expert's span and weight rows past the
 //    expert read as zero with no per-lane predicate.
-//  * LDS is a ring of stages of 32 k (A TM x 64 B + B BNT x 64 B each; four for
-//    a full 256 x 256 tile, six for the 64-row tiles). The loads of k-step
-//    kt+STAGES-1 are issued while k-step kt computes, and the one barrier per
-//    k-step waits only for the stage about to be read (vmcnt leaves the younger
-//    stages in flight), so global latency hides behind STAGES-1 k-steps.
-//  * Rows of 64 bytes hold 4 chunks of 16 bytes; chunk c of row r sits at
-//    physical chunk c ^ ((r >> 2) & 3), so 16 lanes reading 16 consecutive rows
-//    at one chunk touch all 64 banks once (conflict free).
-//  * Fragment reads of the next stage are spread between the MFMAs of the
-//    current one, each well ahead of its use, and a single set of fragment
+//  * LDS holds two rings of 64-k stages: SA stages of A (TM x 128 B each) and
+//    SB >= SA stages of B (BNT x 128 B each); a full 256 x 256 tile uses all
+//    160 KiB as two A and three B stages, smaller tiles up to four of each.
+//    One barrier per stage, placed before the first read of the next stage,
+//    waits for that stage and frees the slots of the one just finished. Their
+//    refills go out while the next stage computes: A (stage SA on) in its
+//    first quarter, B (stage SB on) in its second and third, so every load has
+//    at least three quarters of a stage to land, and B loads SB-1 stages.
+//  * Rows of 128 bytes hold 8 chunks of 16 bytes; chunk c of row r sits at
+//    physical chunk c ^ ((r >> 1) & 7), so 16 lanes reading 16 consecutive rows
+//    at one chunk touch 16 distinct (row parity, chunk) bank groups, all 64
+//    banks once (conflict free).
+//  * Fragment reads of the next 32-k sub-step are spread between the MFMAs of
+//    the current one, each well ahead of its use, and a single set of fragment
 //    registers is live (see ring_tile). sched_barrier fences pin the order.
 //  * The k order of each output's MFMA chain (ascending k in groups of 8, one
 //    accumulator) is the same as the generic path, whatever the tile shape.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format
-constexpr int kRingK = 32;                     // k per LDS stage
+constexpr int kStageK = 64;                    // k per LDS stage
+constexpr int kRowBytes = kStageK * 2;         // one 128-byte line per row and stage
 constexpr int kRingThreads = 256;
-constexpr uint32_t kRingBytes = 128 * 1024;
-// Stages that fit for a tile of TM activation rows and BNT weight rows (k = 32
-// per stage, 64 bytes per row), at most 6.
-constexpr int ring_stages(int tm, int bnt) {
-    const int fit = static_cast<int>(kRingBytes / ((tm + bnt) * kRingK * 2));
-    return fit < 6 ? fit : 6;
+constexpr uint32_t kRingBytes = 160 * 1024;    // all of a gfx950 CU's LDS
+// Ring depths for stages of a_stage (A) and b_stage (B) bytes in `bytes` of
+// LDS: as many B stages as fit beside two A stages (at most 4), then as many A
+// stages as fit beside those (at most the B count).
+constexpr int ring_b_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
+    const int fit = bytes < 2 * a_stage ? 0 : static_cast<int>((bytes - 2 * a_stage) / b_stage);
+    return fit < 4 ? fit : 4;
+}
+constexpr int ring_a_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
+    const int sb = ring_b_stages(a_stage, b_stage, bytes);
+    const int fit = static_cast<int>((bytes - sb * b_stage) / a_stage);
+    return fit < sb ? fit : sb;
 }
 
 // Resource descriptor from wave-uniform values, pinned to SGPRs with readfirstlane
@@ -313,19 +329,20 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst
         0, 0);
 }
 
-// s_waitcnt vmcnt(VM) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] in bits 3:0 and
+// s_waitcnt vmcnt(VM) lgkmcnt(LGKM) (gfx9 encoding: vmcnt[3:0] in bits 3:0 and
 // vmcnt[5:4] in bits 15:14, expcnt in bits 6:4 with 7 = no wait, lgkmcnt in bits 11:8).
-template <int VM>
-__device__ __forceinline__ void wait_vm_lgkm0() {
+template <int VM, int LGKM = 0>
+__device__ __forceinline__ void wait_vm_lgkm() {
     static_assert(VM >= 0 && VM < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4));
+    static_assert(LGKM >= 0 && LGKM < 16, "lgkmcnt range");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LGKM << 8));
 }
 // Workgroup barrier without the implied wait for all memory operations (the
 // explicit wait above bounds what must have landed); the memory clobber keeps
 // the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__device__ __forceinline__ int ring_key(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int ring_key(int row) { return (row >> 1) & 7; }
 
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), unrolled.
 template <typename F, int... I>
@@ -346,13 +363,13 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 
 // One output tile on v_mfma_f32_16x16x32_bf16: rows [row0, row0 + SMT*64) of one
 // expert (clamped to row_end) by BNT weight rows starting at output column
-// col0. A k-step is one 32-k stage: every wave multiplies its (WTM/16) x (WTN/16)
-// grid of 16x16 blocks with one MFMA each while it reads the next stage's
-// fragments and issues loads for a stage AHEAD steps on. The 16x16x32 form
-// sustains a higher clock than 32x32x16 under the power limit (measured on
-// MI355X: 1.91 vs 1.66 GHz with the same read and load mix), so it moves the
-// same FLOPs about 10% faster.
-template <int SMT, int BNT, bool SWIGLU>
+// col0, with a ring in the first LDS_BYTES of `lds`. A 64-k stage is two 32-k
+// sub-steps; in each, every wave multiplies its (WTM/16) x (WTN/16) grid of
+// 16x16 blocks with one MFMA each while it reads the fragments of the next
+// sub-step. The 16x16x32 form sustains a higher clock than 32x32x16 under the
+// power limit (measured on MI355X: 1.91 vs 1.66 GHz with the same read and
+// load mix), so it moves the same FLOPs about 10% faster.
+template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end) {
     constexpr int WAVES = kRingThreads / kWave;
@@ -361,18 +378,27 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     constexpr int WTN = BNT / 2;
     constexpr int FA = WTM / 16;       // 16-row A fragments per wave
     constexpr int FB = WTN / 16;       // 16-row B fragments per wave
-    constexpr int A_LOADS = TM / 16 / WAVES;
-    constexpr int B_LOADS = BNT / 16 / WAVES;
+    constexpr int A_LOADS = TM / 8 / WAVES;    // loads of 8 rows x 128 B per wave and stage
+    constexpr int B_LOADS = BNT / 8 / WAVES;
     constexpr int LOADS = A_LOADS + B_LOADS;
-    constexpr uint32_t A_STAGE = TM * kRingK * 2;   // bytes of one stage of A
-    constexpr uint32_t B_STAGE = BNT * kRingK * 2;  // bytes of one stage of B
-    constexpr int STAGES = ring_stages(TM, BNT) >= 6 ? 6 : 4;  // 4 for 256x256 and 256x128 tiles
-    constexpr int AHEAD = STAGES - 1;               // k-step kt+AHEAD loads during kt
-    constexpr uint32_t B_BASE = STAGES * A_STAGE;   // B stages follow the A stages
+    constexpr uint32_t A_STAGE = TM * kRowBytes;   // bytes of one stage of A
+    constexpr uint32_t B_STAGE = BNT * kRowBytes;  // bytes of one stage of B
+    constexpr int SB = ring_b_stages(A_STAGE, B_STAGE, LDS_BYTES);
+    constexpr int SA = ring_a_stages(A_STAGE, B_STAGE, LDS_BYTES);
+    constexpr uint32_t B_BASE = SA * A_STAGE;      // B stages follow the A stages
+    constexpr uint32_t FRAG = 16 * kRowBytes;      // bytes between 16-row fragments
     static_assert(A_LOADS >= 1 && B_LOADS >= 1 && FA >= 1 && FB >= 2, "tile shape");
     static_assert(!SWIGLU || FB % 2 == 0, "gate/up pairing needs an even fragment count");
-    static_assert(STAGES * (A_STAGE + B_STAGE) <= kRingBytes, "ring does not fit");
-    static_assert((FA - 1) * 1024 < 65536 && (FB - 1) * 1024 < 65536, "fragment offsets fit the instruction offset");
+    static_assert(SA >= 2 && SA <= SB && SA * A_STAGE + SB * B_STAGE <= LDS_BYTES, "ring does not fit");
+    // Loads complete in order. Each stage's window issues A (stage SA on) and
+    // then B (stage SB on). Before stage u+1 is read, its newest loads are its
+    // A loads when SB > SA (its B loads went out SB-SA windows earlier), with
+    // one window's B loads and SA-2 whole windows younger; when SB == SA they
+    // are its B loads, with SA-2 whole windows younger.
+    constexpr int VM_STEADY = (SB > SA ? B_LOADS : 0) + (SA - 2) * LOADS;
+    constexpr int VM_FIRST = (SB > SA ? B_LOADS : 0) + (SA - 1) * LOADS;
+    static_assert(VM_FIRST < 64, "in-flight loads fit the vmcnt field");
+    static_assert((FA - 1) * FRAG < 65536 && (FB - 1) * FRAG < 65536, "fragment offsets fit the instruction offset");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / 2;
@@ -384,18 +410,18 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     const __amdgpu_buffer_rsrc_t rsrc_b =
         make_rsrc(p.b + static_cast<int64_t>(expert) * p.nb * K, static_cast<uint32_t>(p.nb * K * 2));
 
-    const int lrow = lane >> 2;
+    // Load l of a stage covers LDS rows (wave * X_LOADS + l) * 8 + lane / 8.
+    const int lrow = lane >> 3;
+    const int pchunk = lane & 7;
     uint32_t a_off[A_LOADS], b_off[B_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-        const int r = (wave * A_LOADS + i) * 16 + lrow;
-        const int lchunk = (lane & 3) ^ ring_key(r);
-        a_off[i] = static_cast<uint32_t>((r * K + lchunk * 8) * 2);
+        const int r = (wave * A_LOADS + i) * 8 + lrow;
+        a_off[i] = static_cast<uint32_t>((r * K + (pchunk ^ ring_key(r)) * 8) * 2);
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-        const int r = (wave * B_LOADS + i) * 16 + lrow;
-        const int lchunk = (lane & 3) ^ ring_key(r);
+        const int r = (wave * B_LOADS + i) * 8 + lrow;
         int64_t brow;
         if constexpr (SWIGLU) {
             // Wave column wc owns gate columns [wc*WTN/2, (wc+1)*WTN/2) of the
@@ -407,33 +433,32 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         } else {
             brow = col0 + r;
         }
-        b_off[i] = static_cast<uint32_t>((brow * K + lchunk * 8) * 2);
+        b_off[i] = static_cast<uint32_t>((brow * K + (pchunk ^ ring_key(r)) * 8) * 2);
     }
-    // Loads [first, first + count) of the A-then-B list for k-step kt into stage st.
-    auto issue = [&](int kt, int st, int first, int count) {
-        const uint32_t koff = static_cast<uint32_t>(kt) * kRingK * 2;
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            if (i < first || i >= first + count) continue;
-            if (i < A_LOADS)
-                dma16(rsrc_a, lds + st * A_STAGE + (wave * A_LOADS + i) * 1024, a_off[i], koff);
-            else
-                dma16(rsrc_b, lds + B_BASE + st * B_STAGE + (wave * B_LOADS + (i - A_LOADS)) * 1024,
-                      b_off[i - A_LOADS], koff);
-        }
+    // Load l of stage kt into ring slot st, of A and of B.
+    auto issue_a = [&](int kt, int st, int l) {
+        dma16(rsrc_a, lds + st * A_STAGE + (wave * A_LOADS + l) * 1024, a_off[l],
+              static_cast<uint32_t>(kt) * kRowBytes);
+    };
+    auto issue_b = [&](int kt, int st, int l) {
+        dma16(rsrc_b, lds + B_BASE + st * B_STAGE + (wave * B_LOADS + l) * 1024, b_off[l],
+              static_cast<uint32_t>(kt) * kRowBytes);
     };
 
     // Per-lane fragment addresses: lane l reads row (l%16) of a fragment at k
-    // chunk l/16 (all 32 k of the stage in one 16-byte read). Fragments 16 rows
-    // apart share the swizzle key, so fragment and stage only add constants
-    // (instruction offsets); stages from SPLIT on use second bases to keep those
-    // offsets below 64 KiB.
+    // chunk l/16 of the sub-step (all 32 k of it in one 16-byte read). Fragments
+    // 16 rows apart share the swizzle key, so the fragment only adds a constant
+    // (an instruction offset); each ring slot and sub-step has its own base.
     const int frag_row = lane & 15;
     const int chunk = lane >> 4;
     const int ar = wm * WTM + frag_row;
     const int br = wn * WTN + frag_row;
-    const uint32_t va = static_cast<uint32_t>((ar * kRingK + ((chunk ^ ring_key(ar)) << 3)) * 2);
-    const uint32_t vb = B_BASE + static_cast<uint32_t>((br * kRingK + ((chunk ^ ring_key(br)) << 3)) * 2);
+    uint32_t va[2], vb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        va[h] = static_cast<uint32_t>(ar * kRowBytes + (((4 * h + chunk) ^ ring_key(ar)) << 4));
+        vb[h] = B_BASE + static_cast<uint32_t>(br * kRowBytes + (((4 * h + chunk) ^ ring_key(br)) << 4));
+    }
 
     floatx4 acc[FA][FB];
 #pragma unroll
@@ -443,10 +468,8 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
 
-    // Fragment reads at a stage base (per-lane address of stage st, computed
-    // once per k-step); the fragment index is an instruction offset.
     auto read_at = [&](uint32_t base, int idx) {
-        return *reinterpret_cast<const bf16x8_t*>(lds + base + idx * 1024);
+        return *reinterpret_cast<const bf16x8_t*>(lds + base + idx * FRAG);
     };
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
 
@@ -454,67 +477,120 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     // transposed, so lane l holds row l%16 and the four consecutive columns
     // 4*(l/16) + 0..3 (packed 8-byte stores).
     //
-    // One set of fragments (FA A + FB B) is live. A k-step runs in two halves:
-    // B fragments [0, FB/2) with every A fragment, then [FB/2, FB). During the
-    // first half this stage's B fragments [FB/2, FB) are read (their previous
-    // values were last used by the previous step's second half); during the
-    // second half the next stage's A fragment i is read right after its last
-    // MFMA, and the next stage's B fragments [0, FB/2). Every read has at least
-    // about a quarter of a k-step of MFMA work before its first use. The k-loop
-    // is not unrolled (stage addresses are computed per step), so each
-    // accumulator keeps one register through the loop.
+    // One set of fragments (FA A + FB B) is live. A 32-k sub-step runs in two
+    // halves: B fragments [0, FB/2) with every A fragment, then [FB/2, FB).
+    // During the first half this sub-step's B fragments [FB/2, FB) are read
+    // (their previous values were last used by the previous second half);
+    // during the second half the next sub-step's A fragment i is read right
+    // after its last MFMA, and its B fragments [0, FB/2). Every read has at
+    // least about a quarter of a sub-step of MFMA work before its first use.
     constexpr int HB = FB / 2;
-    constexpr int HM = FA * HB;        // MFMAs per half
+    constexpr int HM = FA * HB;        // MFMAs per half sub-step
     static_assert(HB >= 1 && HM >= HB, "half-step shape");
+    static_assert(A_LOADS <= HM && B_LOADS <= 2 * HM, "one load per MFMA slot at most");
     bf16x8_t fa[FA], fb[FB];
-    const int k_steps = static_cast<int>(K / kRingK);
-    // Loads go in two blocks per k-step: one load between each pair of MFMAs
-    // makes the register allocator shuffle the accumulators through copies.
-#pragma unroll
-    for (int st = 0; st < AHEAD; ++st) issue(min(st, k_steps - 1), st, 0, LOADS);
-    wait_vm_lgkm0<(AHEAD - 1) * LOADS>();
-    ring_barrier();
-    fence();
-#pragma unroll
-    for (int i = 0; i < FA; ++i) fa[i] = read_at(va, i);
-#pragma unroll
-    for (int j = 0; j < HB; ++j) fb[j] = read_at(vb, j);
-    int st = 0;
-    for (int kt = 0; kt < k_steps; ++kt) {
-        // k-step kt in stage st; its loads (k-step kt+AHEAD) go to stage
-        // (st+AHEAD)%STAGES, whose reads all ended before the previous barrier.
-        const int nx = st + 1 == STAGES ? 0 : st + 1;
-        const int lst = st == 0 ? STAGES - 1 : st - 1;
-        const int ahead = min(kt + AHEAD, k_steps - 1);
-        const uint32_t b_cur = vb + st * B_STAGE;
-        const uint32_t a_nx = va + nx * A_STAGE, b_nx = vb + nx * B_STAGE;
-        fence();
-        // Stage kt+1 has landed once at most k-steps kt+2 .. kt+AHEAD-1 are younger.
-        wait_vm_lgkm0<(AHEAD - 2) * LOADS>();
-        ring_barrier();
-        fence();
-        issue(ahead, lst, 0, LOADS / 2);
-        fence();
+    // The refills of one window: A loads at evenly spaced MFMA slots of its
+    // first quarter, B loads over the second and third.
+    struct Refill {
+        int kt_a, slot_a, kt_b, slot_b;
+    };
+    auto refill_at = [&](auto g_c, const Refill& r) {
+        constexpr int g = decltype(g_c)::value;  // MFMA slot in the window
+        static_for<A_LOADS>([&](auto l_c) {
+            constexpr int l = decltype(l_c)::value;
+            if constexpr (l * HM / A_LOADS == g) issue_a(r.kt_a, r.slot_a, l);
+        });
+        static_for<B_LOADS>([&](auto l_c) {
+            constexpr int l = decltype(l_c)::value;
+            if constexpr (HM + l * 2 * HM / B_LOADS == g) issue_b(r.kt_b, r.slot_b, l);
+        });
+    };
+    // First half: B [0, HB) x A, reading this sub-step's B [HB, FB) at `bh`.
+    // Quarter q >= 0 of a window carries its share of the refills.
+    auto first_half = [&](uint32_t bh, auto q_c, const Refill& rf) {
+        constexpr int q = decltype(q_c)::value;
         static_for<HM>([&](auto m_c) {
             constexpr int m = decltype(m_c)::value;
             constexpr int i = m / HB, j = m % HB;
+            if constexpr (q >= 0) refill_at(std::integral_constant<int, q * HM + m>{}, rf);
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-            if constexpr (m % 2 == 0 && m / 2 < HB) fb[HB + m / 2] = read_at(b_cur, HB + m / 2);
+            if constexpr (m % 2 == 0 && m / 2 < HB) fb[HB + m / 2] = read_at(bh, HB + m / 2);
             fence();
         });
-        issue(ahead, lst, LOADS / 2, LOADS - LOADS / 2);
-        fence();
+    };
+    // Second half: B [HB, FB) x A, reading the next sub-step's A and B [0, HB)
+    // at (an, bn) unless `last`.
+    auto second_half = [&](uint32_t an, uint32_t bn, auto last_c, auto q_c, const Refill& rf) {
+        constexpr bool last = decltype(last_c)::value;
+        constexpr int q = decltype(q_c)::value;
         static_for<HM>([&](auto m_c) {
             constexpr int m = decltype(m_c)::value;
             constexpr int i = m / HB, j = HB + m % HB;
+            if constexpr (q >= 0) refill_at(std::integral_constant<int, q * HM + m>{}, rf);
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-            if constexpr (m % 2 == 1 && m / 2 < HB) fb[m / 2] = read_at(b_nx, m / 2);
-            if constexpr (m % HB == HB - 1) fa[i] = read_at(a_nx, i);
+            if constexpr (!last) {
+                if constexpr (m % 2 == 1 && m / 2 < HB) fb[m / 2] = read_at(bn, m / 2);
+                if constexpr (m % HB == HB - 1) fa[i] = read_at(an, i);
+            }
             fence();
         });
-        st = nx;
+    };
+
+    const int k_steps = static_cast<int>(K / kStageK);
+    // Prologue: the windows before stage 0, in the steady-state order (A of
+    // stage v+SA, then B of stage v+SB, for v = -SB .. -1). Stages past the
+    // last are loaded as the last one again, so every window issues the same
+    // loads and the vmcnt accounting stays uniform.
+#pragma unroll
+    for (int v = -SB; v < 0; ++v) {
+        if (v + SA >= 0) {
+#pragma unroll
+            for (int l = 0; l < A_LOADS; ++l) issue_a(min(v + SA, k_steps - 1), v + SA, l);
+        }
+#pragma unroll
+        for (int l = 0; l < B_LOADS; ++l) issue_b(min(v + SB, k_steps - 1), v + SB, l);
     }
-    wait_vm_lgkm0<0>();
+    wait_vm_lgkm<VM_FIRST>();
+    ring_barrier();
+    fence();
+    // Sub-step 0's fragments, in the order the second half reads them.
+    static_for<HM>([&](auto m_c) {
+        constexpr int m = decltype(m_c)::value;
+        constexpr int i = m / HB;
+        if constexpr (m % 2 == 1 && m / 2 < HB) fb[m / 2] = read_at(vb[0], m / 2);
+        if constexpr (m % HB == HB - 1) fa[i] = read_at(va[0], i);
+    });
+    // Stage 0 up to its last quarter, then per stage u: [barrier] the last
+    // quarter of stage u (reading stage u+1), then the first three quarters of
+    // stage u+1; this window refills the slots stage u just freed.
+    using NoLoads = std::integral_constant<int, -1>;
+    using More = std::false_type;
+    const Refill none{0, 0, 0, 0};
+    first_half(vb[0], NoLoads{}, none);
+    second_half(va[1], vb[1], More{}, NoLoads{}, none);
+    first_half(vb[1], NoLoads{}, none);
+    int sa = 0, sb = 0;  // ring slots of stage u
+    for (int u = 0; u + 1 < k_steps; ++u) {
+        const int na = sa + 1 == SA ? 0 : sa + 1;
+        const int nb = sb + 1 == SB ? 0 : sb + 1;
+        const Refill rf{min(u + SA, k_steps - 1), sa, min(u + SB, k_steps - 1), sb};
+        const uint32_t a0 = va[0] + na * A_STAGE, a1 = va[1] + na * A_STAGE;
+        const uint32_t b0 = vb[0] + nb * B_STAGE, b1 = vb[1] + nb * B_STAGE;
+        fence();
+        // Stage u+1 has landed, and every read of stage u (the last in the
+        // quarter just done) has returned.
+        wait_vm_lgkm<VM_STEADY>();
+        ring_barrier();
+        fence();
+        second_half(a0, b0, More{}, std::integral_constant<int, 0>{}, rf);
+        first_half(b0, std::integral_constant<int, 1>{}, rf);
+        second_half(a1, b1, More{}, std::integral_constant<int, 2>{}, rf);
+        first_half(b1, std::integral_constant<int, 3>{}, rf);
+        sa = na;
+        sb = nb;
+    }
+    second_half(0u, 0u, std::true_type{}, NoLoads{}, none);
+    wait_vm_lgkm<0>();
 
     // Epilogue: one row per lane, four consecutive columns per 8-byte store.
     // Each row of accumulators is first moved to VGPRs through an empty asm
@@ -642,19 +718,19 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_ring_kernel(GemmPar
     const int rem_rows = span - m_tile * 256;  // rows left from this tile on
     if constexpr (SWIGLU) {
         const int64_t col0 = static_cast<int64_t>(n_tile) * 128;
-        if (rem_rows > 128) ring_tile<4, 256, true>(p, lds, expert, col0, row0, row_end);
-        else if (rem_rows > 64) ring_tile<2, 256, true>(p, lds, expert, col0, row0, row_end);
-        else ring_tile<1, 256, true>(p, lds, expert, col0, row0, row_end);
+        if (rem_rows > 128) ring_tile<4, 256, true, kRingBytes>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) ring_tile<2, 256, true, kRingBytes>(p, lds, expert, col0, row0, row_end);
+        else ring_tile<1, 256, true, kRingBytes>(p, lds, expert, col0, row0, row_end);
     } else if (piece < 0) {
         const int64_t col0 = static_cast<int64_t>(n_tile) * 256;
-        if (rem_rows > 128) ring_tile<4, 256, false>(p, lds, expert, col0, row0, row_end);
-        else if (rem_rows > 64) ring_tile<2, 256, false>(p, lds, expert, col0, row0, row_end);
-        else ring_tile<1, 256, false>(p, lds, expert, col0, row0, row_end);
+        if (rem_rows > 128) ring_tile<4, 256, false, kRingBytes>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) ring_tile<2, 256, false, kRingBytes>(p, lds, expert, col0, row0, row_end);
+        else ring_tile<1, 256, false, kRingBytes>(p, lds, expert, col0, row0, row_end);
     } else {
         const int64_t col0 = static_cast<int64_t>(n_tile) * 256 + piece * 128;
-        if (rem_rows > 128) ring_tile<4, 128, false>(p, lds, expert, col0, row0, row_end);
-        else if (rem_rows > 64) ring_tile<2, 128, false>(p, lds, expert, col0, row0, row_end);
-        else ring_tile<1, 128, false>(p, lds, expert, col0, row0, row_end);
+        if (rem_rows > 128) ring_tile<4, 128, false, kRingBytes>(p, lds, expert, col0, row0, row_end);
+        else if (rem_rows > 64) ring_tile<2, 128, false, kRingBytes>(p, lds, expert, col0, row0, row_end);
+        else ring_tile<1, 128, false, kRingBytes>(p, lds, expert, col0, row0, row_end);
     }
 }
 
@@ -670,9 +746,9 @@ constexpr int kNarrowCols = 64;
 template <bool SWIGLU, int MAX_ROWS>
 __global__ __launch_bounds__(kRingThreads) void grouped_gemm_narrow_kernel(GemmParams p) {
     constexpr int BNT = SWIGLU ? 2 * kNarrowCols : kNarrowCols;
-    constexpr uint32_t kLds = 6 * (MAX_ROWS + BNT) * kRingK * 2;  // six stages of the largest tile
+    constexpr uint32_t kLds = 3 * (MAX_ROWS + BNT) * kRowBytes;  // three stages of the largest tile
     static_assert(MAX_ROWS == 64 || MAX_ROWS == 128, "narrow row tiles");
-    static_assert(ring_stages(MAX_ROWS, BNT) >= 6 && ring_stages(64, BNT) >= 6, "narrow tiles use six stages");
+    static_assert(ring_a_stages(MAX_ROWS * kRowBytes, BNT * kRowBytes, kLds) >= 2, "narrow ring");
     __shared__ __attribute__((aligned(1024))) char lds[kLds];
     const int expert = blockIdx.x / p.n_tiles;
     const int n_tile = blockIdx.x - expert * p.n_tiles;
@@ -684,11 +760,11 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_narrow_kernel(GemmP
     const int64_t col0 = static_cast<int64_t>(n_tile) * kNarrowCols;
     if constexpr (MAX_ROWS == 128) {
         if (span > 64) {
-            ring_tile<2, BNT, SWIGLU>(p, lds, expert, col0, row0, row_end);
+            ring_tile<2, BNT, SWIGLU, kLds>(p, lds, expert, col0, row0, row_end);
             return;
         }
     }
-    ring_tile<1, BNT, SWIGLU>(p, lds, expert, col0, row0, row_end);
+    ring_tile<1, BNT, SWIGLU, kLds>(p, lds, expert, col0, row0, row_end);
 }
 
 // ---------------------------------------------------------------------------
@@ -717,7 +793,7 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     int64_t blocks = m_bound * p.n_tiles;
     if (blocks == 0) return MOE_OK;
     p.n_cu = device_cu_count();
-    if (BM == 256 && BN == 256 && p.k % kRingK == 0 && rows <= 128) {
+    if (BM == 256 && BN == 256 && p.k % kStageK == 0 && rows <= 128) {
         GemmParams q = p;
         q.n_tiles = static_cast<int>((p.n_out + kNarrowCols - 1) / kNarrowCols);
         const int64_t narrow_blocks = static_cast<int64_t>(p.experts) * q.n_tiles;
@@ -730,7 +806,7 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
                                dim3(kRingThreads), 0, stream, q);
         return check_launch("grouped_gemm_narrow_kernel");
     }
-    if (BM == 256 && BN == 256 && p.k % kRingK == 0) {
+    if (BM == 256 && BN == 256 && p.k % kStageK == 0) {
         // Two phases, each rounded up to the XCD count, plus room for the split
         // tail pieces (at most n_cu per phase).
         int64_t ring_blocks = blocks + 2 * kNumXcd;

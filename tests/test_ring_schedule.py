@@ -1,0 +1,84 @@
+"""The grouped GEMM's LDS ring schedule, simulated on the CPU.
+
+ring_tile (cuda-moe-engine_amd/csrc/gemm.hip) keeps SA stages of A and SB >= SA
+stages of B in LDS, issues per stage window the A loads of stage u+SA and then
+the B loads of stage u+SB into the slots stage u freed, and before reading
+stage u+1 waits until at most VM_STEADY loads are outstanding. Loads complete in
+issue order, so the wait is right exactly when no load of stage u+1 is among the
+VM_STEADY newest. This replays the issue order for every tile shape the kernels
+instantiate and checks that each wait covers both matrices of the stage it
+guards and that no refill lands in a slot a still-unread stage occupies. The
+depth and wait formulas below are the kernel's; a wrong count (e.g. treating the
+A loads as the newest when SA == SB) fails here for the affected shapes.
+"""
+
+import itertools
+
+import pytest
+
+KIB = 1024
+ROW_BYTES = 128  # one 64-k stage of one row
+
+
+def b_stages(a_stage, b_stage, lds):
+    fit = 0 if lds < 2 * a_stage else (lds - 2 * a_stage) // b_stage
+    return min(fit, 4)
+
+
+def a_stages(a_stage, b_stage, lds):
+    sb = b_stages(a_stage, b_stage, lds)
+    return min((lds - sb * b_stage) // a_stage, sb)
+
+
+def replay(tm, bnt, lds, k_steps):
+    a_stage, b_stage = tm * ROW_BYTES, bnt * ROW_BYTES
+    sb, sa = b_stages(a_stage, b_stage, lds), a_stages(a_stage, b_stage, lds)
+    a_loads, b_loads = tm // 32, bnt // 32  # 8 rows per load, four waves
+    loads = a_loads + b_loads
+    vm_steady = (b_loads if sb > sa else 0) + (sa - 2) * loads
+    vm_first = (b_loads if sb > sa else 0) + (sa - 1) * loads
+    assert 2 <= sa <= sb and sa * a_stage + sb * b_stage <= lds
+    assert vm_first < 64  # vmcnt field
+
+    issued = []  # [matrix, stage, slot, done]
+
+    def wait(n):
+        for entry in issued[: max(len(issued) - n, 0)]:
+            entry[3] = True
+
+    def landed(matrix, stage):
+        mine = [e for e in issued if e[0] == matrix and e[1] == stage]
+        return bool(mine) and all(e[3] for e in mine)
+
+    for v in range(-sb, 0):  # prologue windows
+        if v + sa >= 0:
+            issued += [["A", v + sa, (v + sa) % sa, False] for _ in range(a_loads)]
+        issued += [["B", v + sb, (v + sb) % sb, False] for _ in range(b_loads)]
+    wait(vm_first)
+    assert landed("A", 0) and landed("B", 0)
+    for u in range(k_steps - 1):
+        wait(vm_steady)
+        assert landed("A", u + 1) and landed("B", u + 1), f"stage {u + 1}"
+        issued += [["A", u + sa, u % sa, False] for _ in range(a_loads)]
+        issued += [["B", u + sb, u % sb, False] for _ in range(b_loads)]
+        assert all(s % sa != u % sa for s in range(u + 1, u + sa))
+        assert all(s % sb != u % sb for s in range(u + 1, u + sb))
+    return sa, sb
+
+
+def _shapes():
+    shapes = {(tm, bnt, 160 * KIB) for tm, bnt in itertools.product((64, 128, 256), (128, 256))}
+    for max_rows, bnt in itertools.product((64, 128), (64, 128)):  # decode tiles
+        lds = 3 * (max_rows + bnt) * ROW_BYTES
+        shapes |= {(64, bnt, lds), (max_rows, bnt, lds)}
+    return sorted(shapes)
+
+
+@pytest.mark.parametrize("tm,bnt,lds", _shapes())
+def test_ring_waits_cover_each_stage(tm, bnt, lds):
+    for k_steps in (1, 2, 3, 4, 5, 7, 64, 224):
+        replay(tm, bnt, lds, k_steps)
+
+
+def test_full_tile_uses_all_lds_as_two_a_and_three_b_stages():
+    assert replay(256, 256, 160 * KIB, 64) == (2, 3)
