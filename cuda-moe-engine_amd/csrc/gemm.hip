@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 //    expert read as zero with no per-lane predicate.
 //  * LDS holds two rings of 64-k stages: SA stages of A (TM x 128 B each) and
 //    SB >= SA stages of B (BNT x 128 B each); a full 256 x 256 tile uses all
-//    160 KiB as two A and three B stages, smaller tiles up to four of each.
+//    160 KiB as two A and three B stages, smaller tiles three or four of each.
 //    One barrier per stage, placed before the first read of the next stage,
 //    waits for that stage and frees the slots of the one just finished. Their
 //    refills go out while the next stage computes: A (stage SA on) in its
@@ -299,13 +299,21 @@ constexpr int kRowBytes = kStageK * 2;         // one 128-byte line per row and 
 constexpr int kRingThreads = 256;
 constexpr uint32_t kRingBytes = 160 * 1024;    // all of a gfx950 CU's LDS
 // Ring depths for stages of a_stage (A) and b_stage (B) bytes in `bytes` of
-// LDS: as many B stages as fit beside two A stages (at most 4), then as many A
-// stages as fit beside those (at most the B count).
+// LDS. When three or more whole stages fit, both rings get that many (at most
+// 4): small tiles compute a stage in a few hundred cycles, so A needs the same
+// lead as B. Otherwise (the 256 x 256 tile) A gets two stages and B as many as
+// fit beside them.
+constexpr int ring_equal_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
+    const int fit = static_cast<int>(bytes / (a_stage + b_stage));
+    return fit < 4 ? fit : 4;
+}
 constexpr int ring_b_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
+    if (ring_equal_stages(a_stage, b_stage, bytes) >= 3) return ring_equal_stages(a_stage, b_stage, bytes);
     const int fit = bytes < 2 * a_stage ? 0 : static_cast<int>((bytes - 2 * a_stage) / b_stage);
     return fit < 4 ? fit : 4;
 }
 constexpr int ring_a_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
+    if (ring_equal_stages(a_stage, b_stage, bytes) >= 3) return ring_equal_stages(a_stage, b_stage, bytes);
     const int sb = ring_b_stages(a_stage, b_stage, bytes);
     const int fit = static_cast<int>((bytes - sb * b_stage) / a_stage);
     return fit < sb ? fit : sb;

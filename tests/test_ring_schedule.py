@@ -1,7 +1,8 @@
 """The grouped GEMM's LDS ring schedule, simulated on the CPU.
 
 ring_tile (cuda-moe-engine_amd/csrc/gemm.hip) keeps SA stages of A and SB >= SA
-stages of B in LDS, issues per stage window the A loads of stage u+SA and then
+stages of B in LDS (equal depths of 3-4 for small tiles, 2 and 3 for the full
+256 x 256 tile), issues per stage window the A loads of stage u+SA and then
 the B loads of stage u+SB into the slots stage u freed, and before reading
 stage u+1 waits until at most VM_STEADY loads are outstanding. Loads complete in
 issue order, so the wait is right exactly when no load of stage u+1 is among the
@@ -20,12 +21,20 @@ KIB = 1024
 ROW_BYTES = 128  # one 64-k stage of one row
 
 
+def equal_stages(a_stage, b_stage, lds):
+    return min(lds // (a_stage + b_stage), 4)
+
+
 def b_stages(a_stage, b_stage, lds):
+    if equal_stages(a_stage, b_stage, lds) >= 3:
+        return equal_stages(a_stage, b_stage, lds)
     fit = 0 if lds < 2 * a_stage else (lds - 2 * a_stage) // b_stage
     return min(fit, 4)
 
 
 def a_stages(a_stage, b_stage, lds):
+    if equal_stages(a_stage, b_stage, lds) >= 3:
+        return equal_stages(a_stage, b_stage, lds)
     sb = b_stages(a_stage, b_stage, lds)
     return min((lds - sb * b_stage) // a_stage, sb)
 
@@ -82,3 +91,8 @@ def test_ring_waits_cover_each_stage(tm, bnt, lds):
 
 def test_full_tile_uses_all_lds_as_two_a_and_three_b_stages():
     assert replay(256, 256, 160 * KIB, 64) == (2, 3)
+
+
+def test_small_tiles_get_equal_depths():
+    assert replay(64, 64, 3 * 128 * ROW_BYTES, 8) == (3, 3)
+    assert replay(64, 256, 160 * KIB, 8) == (4, 4)
