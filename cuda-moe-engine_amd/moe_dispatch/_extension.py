@@ -11,7 +11,6 @@ on the current torch stream without synchronising.
 
 from __future__ import annotations
 
-import hashlib
 from functools import lru_cache
 from pathlib import Path
 
@@ -254,17 +253,9 @@ def get_extension():
     return HipExtension()
 
 
-def source_texts():
-    """Kernel and ABI sources, for provenance hashes."""
-    root = Path(__file__).resolve().parents[1] / "csrc"
-    header = Path(__file__).resolve().parents[2] / "include" / "moe_hip.h"
-    files = sorted(root.glob("*.hip")) + sorted(root.glob("*.h")) + [header]
-    return {f.name: f.read_text() for f in files if f.is_file()}
-
-
 def source_hashes():
-    """sha256 of every kernel source and package module (reference ``_extension.py:18-27``)."""
-    result = {name: hashlib.sha256(text.encode()).hexdigest() for name, text in source_texts().items()}
-    for source in Path(__file__).resolve().parent.glob("*.py"):
-        result[source.name] = hashlib.sha256(source.read_bytes()).hexdigest()
-    return result
+    """sha256 of every kernel source, the ABI header and the package modules
+    (reference ``_extension.py:18-27``); see ``moe_dispatch.evidence.source_files``."""
+    from .evidence import source_hashes as hashes
+
+    return hashes()
