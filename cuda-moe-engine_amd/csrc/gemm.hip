@@ -27,6 +27,7 @@
 #include <type_traits>
 #include <utility>
 
+#include "lds_ring.h"
 #include "moe_common.h"
 
 namespace moe {
@@ -293,7 +294,6 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
 //  * The k order of each output's MFMA chain (ascending k in groups of 8, one
 //    accumulator) is the same as the generic path, whatever the tile shape.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format
 constexpr int kStageK = 64;                    // k per LDS stage
 constexpr int kRowBytes = kStageK * 2;         // one 128-byte line per row and stage
 constexpr int kRingThreads = 256;
@@ -319,48 +319,7 @@ constexpr int ring_a_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) 
     return fit < sb ? fit : sb;
 }
 
-// Resource descriptor from wave-uniform values, pinned to SGPRs with readfirstlane
-// so buffer instructions take it directly (no waterfall loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t addr = reinterpret_cast<uint64_t>(base);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
-    void* uniform_base = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(uniform_base, 0, __builtin_amdgcn_readfirstlane(bytes),
-                                             kRsrcWord3);
-}
-
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst, uint32_t voffset,
-                                      uint32_t soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rsrc, (__attribute__((address_space(3))) void*)(lds_dst), 16, voffset, soffset,
-        0, 0);
-}
-
-// s_waitcnt vmcnt(VM) lgkmcnt(LGKM) (gfx9 encoding: vmcnt[3:0] in bits 3:0 and
-// vmcnt[5:4] in bits 15:14, expcnt in bits 6:4 with 7 = no wait, lgkmcnt in bits 11:8).
-template <int VM, int LGKM = 0>
-__device__ __forceinline__ void wait_vm_lgkm() {
-    static_assert(VM >= 0 && VM < 64, "vmcnt range");
-    static_assert(LGKM >= 0 && LGKM < 16, "lgkmcnt range");
-    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LGKM << 8));
-}
-// Workgroup barrier without the implied wait for all memory operations (the
-// explicit wait above bounds what must have landed); the memory clobber keeps
-// the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
 __device__ __forceinline__ int ring_key(int row) { return (row >> 1) & 7; }
-
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), unrolled.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 // silu(g) * u for the fused epilogue: hardware exp2 and reciprocal
 // (v_exp_f32, v_rcp_f32; about 1 ulp each), g and u already rounded to bf16.

@@ -9,6 +9,7 @@
 #include <climits>
 #include <cmath>
 
+#include "lds_ring.h"
 #include "moe_common.h"
 
 namespace moe {
@@ -111,14 +112,8 @@ __global__ __launch_bounds__(256) void topk_route_kernel(const float* __restrict
 //  * router_split_kernel writes the three planes once per call into the
 //    caller's scratch ([3][E][H] bf16), so the VALU split is not repeated by
 //    every token block.
-//  * router_fused_kernel: a block (4 wavefronts) owns 16 tokens; the waves
-//    split the hidden dimension in interleaved 32-wide slices, their partial
-//    logits are added in a fixed order through LDS, then each wave runs the
-//    top-k of 4 tokens with one lane per expert.
+//  * router_ring_kernel (below) multiplies x by the planes and runs top-k.
 // ---------------------------------------------------------------------------
-typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
-typedef float rfloatx4_t __attribute__((ext_vector_type(4)));
-constexpr int kRouterTokens = 16;
 
 __global__ __launch_bounds__(256) void router_split_kernel(const float* __restrict__ w,
                                                            uint16_t* __restrict__ planes, int64_t n) {
@@ -147,126 +142,223 @@ __global__ __launch_bounds__(256) void router_split_kernel(const float* __restri
     *reinterpret_cast<uint4*>(planes + 2 * n + i) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
 }
 
-// NT expert column tiles of 16 (E <= 16 * NT); MT token tiles of 16 per block,
-// which share each weight slice a block reads from L2.
+// Fused router on an LDS ring. A block owns TB = 16*MT tokens and all experts
+// (EB = 16*NT slots): per 64-k stage, the x rows (TB x 128 B) and the three
+// weight planes (3*EB rows of 128 B, plane q at rows q*EB + e; slots e >= E
+// read as zero) arrive in LDS through direct-to-LDS buffer loads of whole
+// 128-byte lines, so the planes, which every block needs whole, are read from
+// L2 once per block and shared by its waves. Stages sit in a ring of
+// kRouterStages; the loads of stage s + kRouterStages - 1 go out after the
+// barrier that frees stage s - 1's slot.
+//  * The MT x NT output tiles of 16 tokens x 16 experts are spread over the
+//    four waves; when there are fewer than four tiles, G = 4 / tiles waves
+//    share a tile and take every G-th 32-k sub-step, and their partial logits
+//    are added in wave order.
+//  * Per sub-step a tile takes three MFMAs into one accumulator, lo, mid, hi.
+//  * Partial logits go through LDS; then eight lanes per token run the top-k.
+// Rows of 128 bytes hold 8 chunks of 16 bytes; chunk c of row r sits at
+// physical chunk c ^ ((r >> 1) & 7), so 16 lanes reading 16 consecutive rows
+// at one chunk are conflict free.
+typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
+typedef float rfloatx4_t __attribute__((ext_vector_type(4)));
+constexpr int kRouterTokens = 16;
+constexpr int kRouterStages = 4;
+constexpr int kRouterRowBytes = 128;  // 64 k of one row
+constexpr uint32_t kRouterOob = 0x80000000u;  // a buffer offset past any router operand
+
+__device__ __forceinline__ int router_key(int row) { return (row >> 1) & 7; }
+
 template <int NT, int MT>
-__global__ __launch_bounds__(256) void router_fused_kernel(
+struct RouterShape {
+    static constexpr int TB = kRouterTokens * MT;
+    static constexpr int EB = 16 * NT;
+    static constexpr int B_ROWS = 3 * EB;
+    static constexpr int TILES = MT * NT;
+    static constexpr int TPW = TILES >= 4 ? TILES / 4 : 1;  // tiles per wave
+    static constexpr int G = TILES >= 4 ? 1 : 4 / TILES;     // waves per tile
+    static constexpr uint32_t A_STAGE = TB * kRouterRowBytes;
+    static constexpr uint32_t B_STAGE = B_ROWS * kRouterRowBytes;
+    static constexpr uint32_t RING = kRouterStages * (A_STAGE + B_STAGE);
+    static constexpr int LOADS = (TB + B_ROWS) / 8;  // 8 rows per load
+    static constexpr int LPW = LOADS / 4;             // loads per wave and stage
+    static constexpr int EBP = EB + 1;  // partials row stride (floats): lane-per-token reads hit distinct banks
+    static constexpr uint32_t LDS = RING + G * TB * EBP * 4 + EB * 4;  // + bias
+    static_assert(LOADS % 4 == 0, "stage loads split evenly over the waves");
+    static_assert(TILES % 4 == 0 || 4 % TILES == 0, "tiles map onto the waves");
+    static_assert(TPW == 1 || NT % TPW == 0, "a wave's tiles share a token tile");
+    static_assert((kRouterStages - 2) * LPW < 64, "vmcnt range");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <int NT, int MT>
+__global__ __launch_bounds__(256) void router_ring_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ planes,
     const float* __restrict__ bias, int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
     float* __restrict__ weights, float* __restrict__ logits_out, int64_t tokens, int hidden,
     int experts, int topk) {
-    constexpr int TB = kRouterTokens * MT;  // tokens per block
-    __shared__ float part[4][TB][16 * NT];
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
+    using S = RouterShape<NT, MT>;
+    constexpr int TB = S::TB, EB = S::EB, EBP = S::EBP, TPW = S::TPW, G = S::G, LPW = S::LPW;
+    constexpr uint32_t A_STAGE = S::A_STAGE, B_STAGE = S::B_STAGE;
+    constexpr uint32_t B_BASE = kRouterStages * A_STAGE;
+    __shared__ __attribute__((aligned(1024))) char lds[S::LDS];
+    float* part = reinterpret_cast<float*>(lds + S::RING);  // [G][TB][EBP]
+    float* sbias = part + G * TB * EBP;                        // [EB]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TB;
-    const int m = lane & 15;   // A row (token) and B column (expert within a tile)
-    const int kq = lane >> 4;  // 8-element k block within the 32-wide slice
-    const int64_t plane = static_cast<int64_t>(experts) * hidden;
-    const uint16_t* xrow[MT];
-    bool live[MT];
+    const int64_t rows = min(static_cast<int64_t>(TB), tokens - t0);
+    const int64_t row_bytes = static_cast<int64_t>(hidden) * 2;
+    const __amdgpu_buffer_rsrc_t rsrc_x =
+        make_rsrc(x + t0 * hidden, static_cast<uint32_t>(rows * row_bytes));
+    const __amdgpu_buffer_rsrc_t rsrc_w =
+        make_rsrc(planes, static_cast<uint32_t>(3 * static_cast<int64_t>(experts) * row_bytes));
+
+    // This wave's loads: load l covers LDS rows 8*l .. 8*l+7 of the stage
+    // (x rows first, then the plane rows), lane -> row l*8 + lane/8, chunk lane%8.
+    uint32_t voff[LPW];
+    uint32_t ldst[LPW];
+    int kchunk[LPW];  // logical 16-byte chunk (8 k) this lane fetches
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int64_t t = t0 + mt * kRouterTokens + m;
-        live[mt] = t < tokens;
-        xrow[mt] = x + (live[mt] ? t : 0) * static_cast<int64_t>(hidden);
+    for (int j = 0; j < LPW; ++j) {
+        const int l = wave * LPW + j;
+        const int r = l * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ router_key(r);
+        kchunk[j] = chunk;
+        if (l < TB / 8) {
+            voff[j] = static_cast<uint32_t>(r * row_bytes + chunk * 16);
+            ldst[j] = static_cast<uint32_t>(l * 1024);
+        } else {
+            const int br = r - TB;
+            const int q = br / EB, e = br % EB;
+            voff[j] = e < experts ? static_cast<uint32_t>((q * experts + e) * row_bytes + chunk * 16) : kRouterOob;
+            ldst[j] = B_BASE + static_cast<uint32_t>((l - TB / 8) * 1024);
+        }
     }
-
-    rfloatx4_t acc[MT][NT];
+    // A last stage past `hidden` (hidden % 64 != 0) would run into the next
+    // row: its lanes beyond hidden read zero through an out-of-range offset.
+    const int k_stages = (hidden + 63) / 64;
+    const int tail = hidden % 64;
+    auto issue = [&](int stage, int slot) {
+        const uint32_t koff = static_cast<uint32_t>(stage) * kRouterRowBytes;
+        const bool partial = tail != 0 && stage == k_stages - 1;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
-
-    // Slices are visited in batches of kBatch with every load of a batch issued
-    // before its MFMAs, so each wave keeps several 16-byte loads in flight.
-    constexpr int kBatch = NT * MT >= 8 ? 2 : (NT * MT >= 4 ? 4 : 8);
-    auto load8 = [](const uint16_t* src) {
-        rbf16x8_t v;
-        const uint4 raw = *reinterpret_cast<const uint4*>(src);
-        __builtin_memcpy(&v, &raw, 16);
-        return v;
+        for (int j = 0; j < LPW; ++j) {
+            const int l = wave * LPW + j;
+            const uint32_t vo = partial && kchunk[j] * 8 >= tail ? kRouterOob : voff[j];
+            if (l < TB / 8)
+                dma16(rsrc_x, lds + ldst[j] + slot * A_STAGE, vo, koff);
+            else
+                dma16(rsrc_w, lds + ldst[j] + slot * B_STAGE, vo, koff);
+        }
     };
-    rbf16x8_t zero;
+
+    // Tiles of this wave: (token tile mt, expert tiles nt0 .. nt0+TPW-1), k share g.
+    const int tile0 = (wave / G) * TPW;
+    const int mt = tile0 / NT;
+    const int nt0 = tile0 % NT;
+    const int g = wave % G;
+    const int m = lane & 15, kq = lane >> 4;
+    const int ar = mt * 16 + m;
+    uint32_t va[2], vb[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) zero[j] = static_cast<__bf16>(0.0f);
-    for (int kb = wave * 32; kb < hidden; kb += 128 * kBatch) {
-        rbf16x8_t a[kBatch][MT];
-        rbf16x8_t w[kBatch][NT][3];
+    for (int h = 0; h < 2; ++h) {
+        va[h] = static_cast<uint32_t>(ar * kRouterRowBytes + (((4 * h + kq) ^ router_key(ar)) << 4));
+        const int br = nt0 * 16 + m;  // plane 0 row; planes 1, 2 add EB rows (same key: EB % 16 == 0)
+        vb[h] = B_BASE + static_cast<uint32_t>(br * kRouterRowBytes + (((4 * h + kq) ^ router_key(br)) << 4));
+    }
+    rfloatx4_t acc[TPW];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int k = kb + u * 128 + kq * 8;
-            const bool kin = k < hidden;  // hidden % 8 == 0: a block is all in or all out
+    for (int t = 0; t < TPW; ++t) acc[t] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
+
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) a[u][mt] = (live[mt] && kin) ? load8(xrow[mt] + k) : zero;
+    for (int s = 0; s < kRouterStages - 1; ++s) issue(min(s, k_stages - 1), s);
+    for (int s = 0; s < k_stages; ++s) {
+        const int slot = s % kRouterStages;
+        // Stage s has landed once only stages s+1 .. s+kRouterStages-2 are younger;
+        // every read of stage s-1 (whose slot the next loads reuse) has returned.
+        wait_vm_lgkm<(kRouterStages - 2) * LPW>();
+        ring_barrier();
+        issue(min(s + kRouterStages - 1, k_stages - 1), (s + kRouterStages - 1) % kRouterStages);
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const int e = nt * 16 + m;
-                const bool ok = e < experts && kin;
-                const uint16_t* src = planes + static_cast<int64_t>(e) * hidden + k;
+        for (int h = 0; h < 2; ++h) {
+            if ((2 * s + h) % G != g) continue;
+            const char* abase = lds + va[h] + slot * A_STAGE;
+            const char* bbase = lds + vb[h] + slot * B_STAGE;
+            const rbf16x8_t a = *reinterpret_cast<const rbf16x8_t*>(abase);
 #pragma unroll
-                for (int q = 0; q < 3; ++q) w[u][nt][q] = ok ? load8(src + q * plane) : zero;
+            for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+                for (int q = 2; q >= 0; --q) {
+                    const rbf16x8_t b = *reinterpret_cast<const rbf16x8_t*>(
+                        bbase + (q * EB + t * 16) * kRouterRowBytes);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[t], 0, 0, 0);
+                }
             }
         }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u][mt], w[u][nt][2], acc[mt][nt], 0, 0, 0);
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u][mt], w[u][nt][1], acc[mt][nt], 0, 0, 0);
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u][mt], w[u][nt][0], acc[mt][nt], 0, 0, 0);
-                }
     }
-    // 16x16 result: lane l holds tokens 4*(l/16) + r of its token tile, expert column l%16.
+    wait_vm_lgkm<0>();
+    if (threadIdx.x < experts) sbias[threadIdx.x] = bias[threadIdx.x];
+    // 16x16 result: lane l holds tokens 4*(l/16) + r of token tile mt, expert column l%16.
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int t = 0; t < TPW; ++t)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) part[wave][mt * kRouterTokens + 4 * kq + r][nt * 16 + m] = acc[mt][nt][r];
+        for (int r = 0; r < 4; ++r)
+            part[(g * TB + mt * 16 + 4 * kq + r) * EBP + (nt0 + t) * 16 + m] = acc[t][r];
     __syncthreads();
 
-    // Top-k: wave w handles tokens w*TB/4 .. (w+1)*TB/4 - 1, one lane per expert.
-    for (int i = 0; i < TB / 4; ++i) {
-        const int tl = wave * (TB / 4) + i;
-        const int64_t token = t0 + tl;
-        if (token >= tokens) break;
-        float v = -INFINITY;
-        int idx = INT_MAX;
-        if (lane < experts) {
-            const float logit = ((part[0][tl][lane] + part[1][tl][lane]) + part[2][tl][lane]) + part[3][tl][lane];
-            if (logits_out) logits_out[token * experts + lane] = logit;
-            v = logit + bias[lane];
-            idx = lane;
+    // Top-k: eight lanes per token (eight tokens per wave), each lane holding
+    // EB/8 consecutive experts. K rounds of: argmax over the lane's values
+    // (the lower expert wins a tie), the same across the eight lanes with
+    // three xor shuffles, then the winner is removed -- the reference's
+    // iterative argmax with ties to the lower id.
+    constexpr int EPL = EB / 8;
+    static_assert(EPL >= 1 && TB <= 32, "eight lanes per token, at most 32 tokens per block");
+    const int tl = wave * 8 + (lane >> 3);
+    const int sub = lane & 7;
+    const int64_t token = t0 + tl;
+    if (tl < TB && token < tokens) {  // uniform across each group of eight lanes
+        float v[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = sub * EPL + j;
+            v[j] = -INFINITY;
+            if (e < experts) {
+                float logit = part[tl * EBP + e];
+#pragma unroll
+                for (int gg = 1; gg < G; ++gg) logit = logit + part[(gg * TB + tl) * EBP + e];
+                if (logits_out) logits_out[token * experts + e] = logit;
+                v[j] = logit + sbias[e];
+            }
         }
         float sel_v[kMaxTopk];
         int sel_i[kMaxTopk];
 #pragma unroll
         for (int k = 0; k < kMaxTopk; ++k) {
             if (k < topk) {
-                float bv = v;
-                int bi = idx;
+                float bv = v[0];
+                int bi = sub * EPL;
 #pragma unroll
-                for (int msk = 32; msk >= 1; msk >>= 1) {
+                for (int j = 1; j < EPL; ++j) {
+                    const bool take = v[j] > bv;
+                    bv = take ? v[j] : bv;
+                    bi = take ? sub * EPL + j : bi;
+                }
+#pragma unroll
+                for (int msk = 1; msk < 8; msk <<= 1) {
                     const float ov = __shfl_xor(bv, msk);
                     const int oi = __shfl_xor(bi, msk);
-                    if (ov > bv || (ov == bv && oi < bi)) {
-                        bv = ov;
-                        bi = oi;
-                    }
+                    const bool take = ov > bv || (ov == bv && oi < bi);
+                    bv = take ? ov : bv;
+                    bi = take ? oi : bi;
                 }
                 sel_v[k] = bv;
                 sel_i[k] = bi;
-                if (idx == bi) {
-                    v = -INFINITY;
-                    idx = INT_MAX;
-                }
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) v[j] = (sub * EPL + j == bi) ? -INFINITY : v[j];
             }
         }
-        if (lane == 0) write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
+        if (sub == 0) write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
     }
 }
 
@@ -317,24 +409,27 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
                        stream, router_w, planes, n);
     const int rc = check_launch("router_split_kernel");
     if (rc != MOE_OK) return rc;
-    // One token tile per block: measured at E=64, H=2048, T=8192, four tiles per
-    // block (fewer, longer blocks) ran 1.5x slower than one.
+    // Buffer offsets are 32-bit: 3*E*H*2 bytes of planes and 32 rows of x must fit.
+    MOE_REQUIRE(hidden <= (1 << 20), MOE_ERR_UNSUPPORTED, "fused router supports hidden <= 1048576 (got %d)",
+                hidden);
 #define MOE_ROUTER_CASE(NTV, MTV)                                                                      \
-    hipLaunchKernelGGL((router_fused_kernel<NTV, MTV>),                                                \
+    hipLaunchKernelGGL((router_ring_kernel<NTV, MTV>),                                                 \
                        dim3(static_cast<unsigned>((tokens + kRouterTokens * MTV - 1) / (kRouterTokens * MTV))), \
                        dim3(256), 0, stream, x, planes, bias, ids32, ids64, weights, logits_out, tokens, \
                        hidden, experts, topk)
+    // Token tiles per block: one for E <= 16 (the four waves split k), two
+    // above (the waves split the 16x16 output tiles).
     if (experts <= 16) {
         MOE_ROUTER_CASE(1, 1);
     } else if (experts <= 32) {
-        MOE_ROUTER_CASE(2, 1);
+        MOE_ROUTER_CASE(2, 2);
     } else if (experts <= 64) {
-        MOE_ROUTER_CASE(4, 1);
+        MOE_ROUTER_CASE(4, 2);
     } else {
         return fail(MOE_ERR_UNSUPPORTED, "experts=%d exceeds 64", experts);
     }
 #undef MOE_ROUTER_CASE
-    return check_launch("router_fused_kernel");
+    return check_launch("router_ring_kernel");
 }
 
 }  // namespace moe

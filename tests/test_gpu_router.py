@@ -67,7 +67,7 @@ def test_zero_logits_known_answer_and_empty_batch(ext):
 @pytest.mark.parametrize(
     "tokens,hidden,experts,topk",
     [(1, 512, 8, 2), (33, 512, 8, 1), (257, 1024, 16, 2), (300, 2048, 64, 6), (64, 4096, 8, 2),
-     (100, 136, 5, 3)],
+     (100, 136, 5, 3), (1000, 72, 32, 4), (8192, 2048, 64, 6)],
 )
 def test_fused_router_matches_oracle(ext, tokens, hidden, experts, topk):
     generator = torch.Generator(device="cuda").manual_seed(tokens + hidden)
@@ -93,3 +93,22 @@ def test_fused_router_matches_oracle(ext, tokens, hidden, experts, topk):
     ids_ref, _, _ = oracle.topk_route(ref_logits, to_np(bias), topk)
     safe = route_margin(ref_logits, to_np(bias), topk) > 1e-4
     np.testing.assert_array_equal(np.sort(to_np(ids32)[safe], 1), np.sort(ids_ref[safe], 1))
+
+
+@pytest.mark.parametrize("experts,topk", [(8, 2), (16, 5), (32, 4), (64, 6), (64, 8)])
+def test_fused_router_ties_go_to_lower_expert(ext, experts, topk):
+    """Zero activations make every logit exactly 0, so the selection is decided by a
+    bias full of repeated values: the fused top-k must keep the lower expert id on
+    every tie, like the reference (``csrc/dispatch.cu:331-333``)."""
+    tokens, hidden = 70, 128
+    x = torch.zeros(tokens, hidden, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(experts, hidden, device="cuda") / hidden**0.5
+    levels = torch.tensor([0.0, 1.0, 2.0, 0.5], device="cuda")
+    bias = levels[torch.arange(experts, device="cuda") * 7 % 4].contiguous()
+    ids32 = torch.empty(tokens, topk, device="cuda", dtype=torch.int32)
+    ids64 = torch.empty(tokens, topk, device="cuda", dtype=torch.int64)
+    weights = torch.empty(tokens, topk, device="cuda")
+    ext.router_fused_out(x, w, bias, ids32, ids64, weights)
+    ids_ref, w_ref, _ = oracle.topk_route(np.zeros((tokens, experts), np.float32), to_np(bias), topk)
+    np.testing.assert_array_equal(to_np(ids32), ids_ref)
+    np.testing.assert_allclose(to_np(weights), w_ref, rtol=2e-6, atol=2e-6)
