@@ -190,6 +190,9 @@ int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offse
     MOE_REQUIRE(rows >= 0 && rows <= INT_MAX, MOE_ERR_CAPACITY, "rows exceed int32");
     MOE_REQUIRE(n > 0 && k > 0 && n % 8 == 0 && k % 8 == 0, MOE_ERR_UNSUPPORTED,
                 "grouped GEMM dimensions must be positive multiples of 8");
+    // The kernels bound each expert's weights and row tile with 32-bit buffer ranges.
+    MOE_REQUIRE(n <= INT_MAX && k <= INT_MAX && n * k * 2 <= UINT32_MAX && 256 * k * 2 <= UINT32_MAX,
+                MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
     if (rows == 0) return MOE_OK;
     MOE_REQUIRE(a && b && c && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
     return launch_grouped_gemm(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
@@ -204,6 +207,9 @@ int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
     MOE_REQUIRE(rows >= 0 && rows <= INT_MAX, MOE_ERR_CAPACITY, "rows exceed int32");
     MOE_REQUIRE(hidden > 0 && intermediate > 0 && hidden % 8 == 0 && intermediate % 8 == 0,
                 MOE_ERR_UNSUPPORTED, "grouped GEMM dimensions must be positive multiples of 8");
+    MOE_REQUIRE(hidden <= INT_MAX && intermediate <= INT_MAX && 2 * intermediate * hidden * 2 <= UINT32_MAX &&
+                    256 * hidden * 2 <= UINT32_MAX,
+                MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
     if (rows == 0) return MOE_OK;
     MOE_REQUIRE(a && gate_up && act && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
     return launch_gateup_swiglu(static_cast<const uint16_t*>(a),

@@ -57,6 +57,11 @@ def test_validation_errors_without_launching():
     assert lib.moe_dispatch(1, 7, 1, 1, 1, 1, 1, 1, 1, need, 10, 64, 8, 2, 8, 80, 1, None) == 1
     assert lib.moe_grouped_gemm(1, 1, 1, 1, 16, 12, 64, 8, None) == 2
     assert lib.moe_grouped_gateup_swiglu(1, 1, 1, 1, 16, 64, 64, 65, None) == 2
+    # One expert's weights of 4 GiB or more do not fit the kernels' 32-bit buffer ranges.
+    assert lib.moe_grouped_gemm(1, 1, 1, 1, 16, 1 << 16, 1 << 15, 8, None) == 3
+    assert b"4 GiB" in lib.moe_last_error()
+    assert lib.moe_grouped_gateup_swiglu(1, 1, 1, 1, 16, 1 << 15, 1 << 15, 8, None) == 3
+    assert lib.moe_grouped_gemm(1, 1, 1, 0, 0, 1 << 15, 1 << 15, 8, None) == 0  # 2 GiB: accepted (no rows)
     # hidden 12 is not a multiple of 8; then a scratch buffer below the split's size.
     assert lib.moe_router_fused(1, 1, 1, 1, 1, 1, None, 16, 1 << 20, 4, 12, 8, 2, None) == 2
     assert lib.moe_router_scratch_bytes(8, 64) == 3 * 8 * 64 * 2

@@ -38,7 +38,7 @@ def test_measured_traffic_sums_kernels(tmp_path, monkeypatch):
 
 def test_committed_traffic_table_covers_the_bench_kernels():
     table = json.loads((ROOT / "profiles" / "hbm_traffic.json").read_text())
-    assert "grouped_gemm_ring_kernel<true>" in table["c4_t4096"]
+    assert "grouped_gemm_persistent_kernel<true>" in table["c4_t4096"]
     assert {"count_rank_kernel", "pack_kernel<16>"} <= set(table["c2_transport"])
 
 
@@ -56,6 +56,6 @@ def test_gateup_roofline_picks_the_bound_by_intensity():
     # Prefill: 8192 assignments over 8 experts is far past the ridge point.
     pre = bench.gateup_roofline("none", np.array([1024] * 8), 8248, h, i, 8192, 4.0 * 8192 * h * i, 1000.0)
     assert pre["bound"] == "mfma" and pre["unit"] == "TFLOP/s"
-    assert pre["kernel"].startswith("grouped_gemm_ring_kernel<true>")
+    assert pre["kernel"].startswith("grouped_gemm_persistent_kernel<true>")
     assert abs(pre["achieved"] - 4.0 * 8192 * h * i / 1e-3 / 1e12) < 0.1
     assert list(pre)[0] == "bound"
