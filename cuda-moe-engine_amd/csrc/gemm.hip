@@ -338,13 +338,14 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // load mix), so it moves the same FLOPs about 10% faster.
 // The ring's shape and direct-to-LDS loads for one tile: rows [row0,
 // row0 + SMT*64) of one expert (clamped to row_end) by BNT weight rows from
-// output column col0, in the first LDS_BYTES of `lds`.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES>
+// output column col0, in the first LDS_BYTES of `lds`. The four waves split
+// the tile as (4/WC) row blocks x WC column blocks.
+template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2>
 struct RingOps {
     static constexpr int WAVES = kRingThreads / kWave;
     static constexpr int TM = SMT * 64;
-    static constexpr int WTM = TM / 2;
-    static constexpr int WTN = BNT / 2;
+    static constexpr int WTM = TM / (WAVES / WC);  // the four waves as (4/WC) x WC
+    static constexpr int WTN = BNT / WC;
     static constexpr int FA = WTM / 16;       // 16-row A fragments per wave
     static constexpr int FB = WTN / 16;       // 16-row B fragments per wave
     static constexpr int A_LOADS = TM / 8 / WAVES;    // loads of 8 rows x 128 B per wave and stage
@@ -446,11 +447,11 @@ struct NoHook {
 // before the first read instead of counting loads. hook: runs once the
 // k-loop is done and every wave has finished with the ring (it may refill
 // LDS), before the epilogue.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook>
+template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end, bool own_prologue = true,
                                           bool wait_all = false, const Hook& hook = Hook{}) {
-    using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES>;
+    using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC>;
     constexpr int WTM = R::WTM, WTN = R::WTN, FA = R::FA, FB = R::FB;
     constexpr int A_LOADS = R::A_LOADS, B_LOADS = R::B_LOADS;
     constexpr int SA = R::SA, SB = R::SB;
@@ -458,8 +459,8 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     constexpr int VM_STEADY = R::VM_STEADY, VM_FIRST = R::VM_FIRST;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave / 2;
-    const int wn = wave % 2;
+    const int wm = wave / WC;
+    const int wn = wave % WC;
     const int64_t K = p.k;
     const R ops(p, lds, expert, col0, row0, row_end);
     auto issue_a = [&](int kt, int st, int l) { ops.issue_a(kt, st, l); };
@@ -507,7 +508,16 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     constexpr int HB = FB / 2;
     constexpr int HM = FA * HB;        // MFMAs per half sub-step
     static_assert(HB >= 1 && HM >= HB, "half-step shape");
-    static_assert(A_LOADS <= HM && B_LOADS <= 2 * HM, "one load per MFMA slot at most");
+    // MFMA slots of the B fragment reads: this sub-step's fragment HB+b in
+    // the first half, the next sub-step's fragment b in the second, one every
+    // other MFMA (all at the last MFMA of a half that has fewer).
+    constexpr auto first_read_slot = [](int b) constexpr { return 2 * b < HM - 1 ? 2 * b : HM - 1; };
+    constexpr auto second_read_slot = [](int b) constexpr { return 2 * b + 1 < HM - 1 ? 2 * b + 1 : HM - 1; };
+    constexpr int LOADS = A_LOADS + B_LOADS;
+    // Slots of a window's loads: A in its first quarter and B in its second
+    // and third when they fit one per MFMA; otherwise all spread evenly, A
+    // first (small tiles with few MFMAs per quarter).
+    constexpr bool kQuarters = A_LOADS <= HM && B_LOADS <= 2 * HM;
     bf16x8_t fa[FA], fb[FB];
     // The refills of one window: A loads at evenly spaced MFMA slots of its
     // first quarter, B loads over the second and third.
@@ -518,11 +528,13 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         constexpr int g = decltype(g_c)::value;  // MFMA slot in the window
         static_for<A_LOADS>([&](auto l_c) {
             constexpr int l = decltype(l_c)::value;
-            if constexpr (l * HM / A_LOADS == g) issue_a(r.kt_a, r.slot_a, l);
+            constexpr int slot = kQuarters ? l * HM / A_LOADS : l * 4 * HM / LOADS;
+            if constexpr (slot == g) issue_a(r.kt_a, r.slot_a, l);
         });
         static_for<B_LOADS>([&](auto l_c) {
             constexpr int l = decltype(l_c)::value;
-            if constexpr (HM + l * 2 * HM / B_LOADS == g) issue_b(r.kt_b, r.slot_b, l);
+            constexpr int slot = kQuarters ? HM + l * 2 * HM / B_LOADS : (A_LOADS + l) * 4 * HM / LOADS;
+            if constexpr (slot == g) issue_b(r.kt_b, r.slot_b, l);
         });
     };
     // First half: B [0, HB) x A, reading this sub-step's B [HB, FB) at `bh`.
@@ -534,7 +546,10 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
             constexpr int i = m / HB, j = m % HB;
             if constexpr (q >= 0) refill_at(std::integral_constant<int, q * HM + m>{}, rf);
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-            if constexpr (m % 2 == 0 && m / 2 < HB) fb[HB + m / 2] = read_at(bh, HB + m / 2);
+            static_for<HB>([&](auto b_c) {
+                constexpr int b = decltype(b_c)::value;
+                if constexpr (first_read_slot(b) == m) fb[HB + b] = read_at(bh, HB + b);
+            });
             fence();
         });
     };
@@ -549,7 +564,10 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
             if constexpr (q >= 0) refill_at(std::integral_constant<int, q * HM + m>{}, rf);
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
             if constexpr (!last) {
-                if constexpr (m % 2 == 1 && m / 2 < HB) fb[m / 2] = read_at(bn, m / 2);
+                static_for<HB>([&](auto b_c) {
+                    constexpr int b = decltype(b_c)::value;
+                    if constexpr (second_read_slot(b) == m) fb[b] = read_at(bn, b);
+                });
                 if constexpr (m % HB == HB - 1) fa[i] = read_at(an, i);
             }
             fence();
@@ -568,7 +586,10 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     static_for<HM>([&](auto m_c) {
         constexpr int m = decltype(m_c)::value;
         constexpr int i = m / HB;
-        if constexpr (m % 2 == 1 && m / 2 < HB) fb[m / 2] = read_at(vb[0], m / 2);
+        static_for<HB>([&](auto b_c) {
+            constexpr int b = decltype(b_c)::value;
+            if constexpr (second_read_slot(b) == m) fb[b] = read_at(vb[0], b);
+        });
         if constexpr (m % HB == HB - 1) fa[i] = read_at(va[0], i);
     });
     // Stage 0 up to its last quarter, then per stage u: [barrier] the last
@@ -879,17 +900,23 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
 }
 
 // Decode-sized launches (at most 128 rows in all): every expert has at most one
-// row tile, so the work is streaming the active experts' weights. Tiles are 64
-// output columns wide, four times as many as the 256-wide tiles, so that a
-// single token's two experts still spread over the CUs. Each output is the
-// same MFMA chain in k order as on the wide path. MAX_ROWS (64 or 128) bounds
-// every expert's span; the 64-row instance needs less LDS, so more blocks share
-// a CU.
-constexpr int kNarrowCols = 64;
+// row tile, so the work is streaming the active experts' weights. Tiles are
+// narrow so that a single token's two experts still spread over the CUs: 64
+// activation columns (128 weight rows, waves 2 x 2) for the gate/up GEMM, 64
+// output columns for the down GEMM, and 32 (waves 4 x 1) when at most 64 rows
+// are packed (measured at T=1: down 54.7 -> 51.8 us; at T=16 the 4 x 1 waves,
+// which all read every B fragment, ran 7% slower than 64 columns). Each output
+// is the same MFMA chain in k order as on the wide path. MAX_ROWS (64 or 128)
+// bounds every expert's span; the 64-row instance needs less LDS, so more
+// blocks share a CU.
+template <bool SWIGLU, int MAX_ROWS>
+constexpr int narrow_cols() { return SWIGLU || MAX_ROWS == 128 ? 64 : 32; }
 
 template <bool SWIGLU, int MAX_ROWS>
 __global__ __launch_bounds__(kRingThreads) void grouped_gemm_narrow_kernel(GemmParams p) {
-    constexpr int BNT = SWIGLU ? 2 * kNarrowCols : kNarrowCols;
+    constexpr int COLS = narrow_cols<SWIGLU, MAX_ROWS>();
+    constexpr int BNT = SWIGLU ? 2 * COLS : COLS;
+    constexpr int WC = BNT == 32 ? 1 : 2;
     constexpr uint32_t kLds = 3 * (MAX_ROWS + BNT) * kRowBytes;  // three stages of the largest tile
     static_assert(MAX_ROWS == 64 || MAX_ROWS == 128, "narrow row tiles");
     static_assert(ring_a_stages(MAX_ROWS * kRowBytes, BNT * kRowBytes, kLds) >= 2, "narrow ring");
@@ -901,14 +928,14 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_narrow_kernel(GemmP
     const int64_t row_end = min(static_cast<int64_t>(p.offsets[expert + 1]), p.rows);
     if (row0 < 0 || row0 >= row_end) return;
     const int64_t span = row_end - row0;  // <= p.rows <= MAX_ROWS (checked by the launcher)
-    const int64_t col0 = static_cast<int64_t>(n_tile) * kNarrowCols;
+    const int64_t col0 = static_cast<int64_t>(n_tile) * COLS;
     if constexpr (MAX_ROWS == 128) {
         if (span > 64) {
-            ring_tile<2, BNT, SWIGLU, kLds>(p, lds, expert, col0, row0, row_end);
+            ring_tile<2, BNT, SWIGLU, kLds, NoHook, WC>(p, lds, expert, col0, row0, row_end);
             return;
         }
     }
-    ring_tile<1, BNT, SWIGLU, kLds>(p, lds, expert, col0, row0, row_end);
+    ring_tile<1, BNT, SWIGLU, kLds, NoHook, WC>(p, lds, expert, col0, row0, row_end);
 }
 
 // ---------------------------------------------------------------------------
@@ -939,7 +966,8 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     p.n_cu = device_cu_count();
     if (BM == 256 && BN == 256 && p.k % kStageK == 0 && rows <= 128) {
         GemmParams q = p;
-        q.n_tiles = static_cast<int>((p.n_out + kNarrowCols - 1) / kNarrowCols);
+        const int cols = rows <= 64 ? narrow_cols<SWIGLU, 64>() : narrow_cols<SWIGLU, 128>();
+        q.n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
         const int64_t narrow_blocks = static_cast<int64_t>(p.experts) * q.n_tiles;
         if (narrow_blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
         if (rows <= 64)

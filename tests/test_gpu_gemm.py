@@ -6,7 +6,7 @@ rest one bf16 step away (see tests/_helpers.assert_near_bit_exact); and,
 independently, within one bf16 rounding of the exact float64 product. Covers empty experts,
 skewed row counts, partial row tiles, short reductions (K < 64), column counts
 that are not multiples of the column tile, decode-sized launches (at most 128
-rows, which take 64-column tiles), and the fused gate/up + SwiGLU
+rows, which take 32- and 64-column tiles), and the fused gate/up + SwiGLU
 epilogue against the kernels' own unfused pipeline (grouped GEMM -> bf16
 projection -> standalone SwiGLU). The two see the same bf16 gate and up values;
 the fused epilogue evaluates silu with the hardware exp2 and reciprocal
@@ -46,9 +46,12 @@ GEMM_CASES = [
     ([1024, 1030, 998, 1051], 8, 264, 200),
     ([33] * 16, 1, 128, 1024),
     ([2000, 0], 8, 1024, 512),
-    # at most 128 rows in all: the 64-column decode tiles
+    # at most 128 rows in all: the 32-column decode tiles (K % 64 == 0; K=96 takes the generic path)
     ([90, 20, 0], 8, 200, 96),
     ([1, 0, 1], 1, 1000, 64),
+    ([90, 20, 0], 8, 200, 128),
+    ([7, 0, 40], 1, 96, 192),
+    ([2, 2], 1, 4096, 1024),
 ]
 
 

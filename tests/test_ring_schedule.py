@@ -77,7 +77,7 @@ def replay(tm, bnt, lds, k_steps):
 
 def _shapes():
     shapes = {(tm, bnt, 160 * KIB) for tm, bnt in itertools.product((64, 128, 256), (128, 256))}
-    for max_rows, bnt in itertools.product((64, 128), (64, 128)):  # decode tiles
+    for max_rows, bnt in ((64, 32), (128, 64), (64, 128), (128, 128)):  # decode tiles (down, gate/up)
         lds = 3 * (max_rows + bnt) * ROW_BYTES
         shapes |= {(64, bnt, lds), (max_rows, bnt, lds)}
     return sorted(shapes)
