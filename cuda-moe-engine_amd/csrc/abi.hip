@@ -25,6 +25,7 @@ int launch_grouped_gemm(const uint16_t*, const uint16_t*, uint16_t*, const int32
                         int64_t, int64_t, int, hipStream_t);
 int launch_gateup_swiglu(const uint16_t*, const uint16_t*, uint16_t*, const int32_t*, int64_t,
                          int64_t, int64_t, int, hipStream_t);
+void set_gemm_workgroup_limit(int);
 
 static thread_local char g_last_error[512] = "";
 
@@ -216,6 +217,13 @@ int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
                                 static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(act),
                                 offsets, rows, hidden, intermediate, (int)experts,
                                 static_cast<hipStream_t>(stream));
+}
+
+int moe_set_gemm_workgroups(int64_t workgroups) {
+    MOE_REQUIRE(workgroups >= 0 && workgroups <= INT_MAX, MOE_ERR_INVALID_ARGUMENT,
+                "workgroups must be in [0, INT_MAX]");
+    set_gemm_workgroup_limit(static_cast<int>(workgroups));
+    return MOE_OK;
 }
 
 }  // extern "C"

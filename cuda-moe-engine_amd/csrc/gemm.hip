@@ -14,16 +14,19 @@
 //    below -- 256 x 256 tiles on four wavefronts of 128 x 128 (16x16x32 MFMAs),
 //    direct-to-LDS buffer loads of whole 128-byte lines into an LDS ring of
 //    64-k stages, MFMAs interleaved with fragment reads and loads, XCD-aware
-//    two-phase order; 64-column tiles for decode-sized launches.
+//    rounds of full row tiles with the experts' short last row tiles carried
+//    beside them; 32- and 64-column tiles for decode-sized launches.
 //  * Generic path (any K % 8 == 0): grouped_gemm_kernel -- global -> register ->
 //    LDS double buffering with one barrier per 64-wide k-step; LDS rows are 128
 //    bytes with 16-byte chunks XOR-swizzled per row (swz).
 //  * Tile schedule is built on the device from offsets: expert e contributes
-//    ceil(span_e/256) row tiles per column tile (0 for an empty expert). The grid
-//    is a host-side upper bound; surplus workgroups exit at once, and no offsets
-//    are read on the host.
+//    ceil(span_e/256) row tiles per column tile (0 for an empty expert). No
+//    offsets are read on the host: the generic grid is an upper bound whose
+//    surplus workgroups exit at once, and the persistent grid is one workgroup
+//    per CU.
 //  * Every output element is one MFMA chain in ascending k with one fp32
 //    accumulator, whichever path and tile shape computes it.
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -51,7 +54,6 @@ struct GemmParams {
     int64_t rows;             // rows of A and C; spans are clamped to it
     int experts;
     int n_tiles;              // output column tiles
-    int n_cu;                 // compute units of the device (tail balancing)
 };
 
 // 16-byte chunk c of LDS row r lives at physical chunk c ^ f(r), f(r) = (r ^ (r >> 3)) & 7.
@@ -667,42 +669,142 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     }
 }
 
-// Work list, built on the device from offsets. Row tiles of more than 128 rows
-// form phase 1 (equal cost) and the short last row tile of an expert (at most
-// 128 rows) forms phase 2, so the CUs of an XCD run phase-1 tiles in lockstep
-// rounds and share A and B k-slices in L2. Inside a phase, tiles go expert by
-// expert, column tile by column tile, row tiles fastest, and each phase is
-// spread over the XCDs in contiguous ranges (workgroup i runs on XCD i % 8).
-// For the plain GEMM a short last round of a phase (at most half of the CUs)
-// is split into 128-column pieces; every piece still runs the whole k chain
-// in order, so results do not change.
+// Work list, built on the device from offsets (the same in every workgroup).
+// Row tiles of more than 128 rows form phase 1: they all cost the same and are
+// compute-bound. The short last row tile of an expert (at most 128 rows) forms
+// phase 2: it reads a whole 256-row weight slab for a quarter or half of the
+// arithmetic, so its cost is streaming that slab at one CU's request rate
+// (about half of a phase-1 tile: 49 vs 101 us at H=4096, I=14336), and many of
+// them at once are HBM-bound.
+//
+// The grid (G workgroups, workgroup i on XCD i % 8) walks virtual workgroups
+// q = blockIdx.x, blockIdx.x + G, ..., i.e. in rounds of G. Phase 1 is cut
+// into 8 contiguous ranges, one per XCD, and each XCD runs its range in order,
+// cpr tiles per round, so the CUs of an XCD run neighbouring tiles (same
+// expert and column tile, adjacent row tiles) in lockstep and share A and B
+// k-slices in L2. The other slots of the rounds take one or two phase-2 tiles
+// each, so their weight streaming runs beside the compute-bound tiles, within
+// the HBM headroom, instead of after them at the HBM limit. The round count is
+// the minimum for phase 1, plus one when more than one phase-2 tile per
+// workgroup would otherwise be left over; leftover phase-2 tiles run after the
+// rounds, one per slot. Inside a phase, tiles go expert by expert, column tile
+// by column tile, row tiles fastest. Measured at H=4096, I=14336, 4096 tokens:
+// the short tiles took 250 us after the 1418 us of phase 1 when run last.
+//
+// For the plain GEMM a short last round (at most half of the slots busy) of
+// phase 1 (when there is no phase 2) or of the leftover phase-2 tiles is split
+// into 128-column pieces. Every tile or piece runs its whole k chain in order
+// on one workgroup, so results do not depend on the schedule or on G.
 struct RingPhase {
     int count;   // tiles
     int main;    // tiles mapped XCD-contiguously
-    int blocks;  // workgroups of the main part (multiple of 8)
+    int blocks;  // virtual workgroups of the main part (multiple of 8)
     int pieces;  // split tail pieces (2 per split tile)
 };
 
-__device__ __forceinline__ RingPhase ring_phase(int count, int n_cu, bool allow_split) {
+__device__ __forceinline__ RingPhase ring_phase(int count, int grid, bool allow_split) {
     RingPhase ph;
     ph.count = count;
-    const int rem = n_cu > 0 ? count % n_cu : 0;
-    const bool split = allow_split && rem > 0 && 2 * rem <= n_cu;
+    const int rem = count % grid;
+    const bool split = allow_split && rem > 0 && 2 * rem <= grid;
     ph.main = split ? count - rem : count;
     ph.blocks = (ph.main + kNumXcd - 1) / kNumXcd * kNumXcd;
     ph.pieces = split ? 2 * rem : 0;
     return ph;
 }
 
-// The fast-path kernel is persistent: one workgroup per CU walks the virtual
-// workgroups q = blockIdx.x, blockIdx.x + gridDim.x, ... (the tiles, and the
-// XCDs they run on, of one workgroup per virtual workgroup) and, once
-// a tile's k-loop is done, issues the next tile's first stages before running
-// the epilogue, so their latency hides behind the epilogue's arithmetic and
-// stores, and the per-workgroup start-up is paid once per CU. Tiles are
-// decoded from a per-wave table (lane e = expert e) instead of a loop over
-// the offsets per tile. Measured: C3 and C5 expert GEMMs 5-11% faster, C4
-// T=4096 about 1%.
+struct RingPlan {
+    int n1;           // phase-1 tiles
+    int n2;           // phase-2 tiles
+    int per1;         // phase-1 tiles per XCD range
+    int cpr;          // phase-1 tiles per XCD and round
+    int rounds;       // interleaved rounds (0: none)
+    int full_rounds;  // rounds that run cpr phase-1 tiles per XCD
+    int last_cols;    // phase-1 tiles per XCD in round full_rounds
+    int slots;        // phase-2 slots in the rounds
+    int carried;      // phase-2 tiles the rounds take (at most two per slot)
+    RingPhase rest;   // after the rounds: phase 1 (no phase 2) or the leftover phase-2 tiles
+    int virtual_blocks;
+};
+
+// grid is a positive multiple of 8.
+__device__ __forceinline__ RingPlan ring_plan(int n1, int n2, int grid, bool allow_split) {
+    RingPlan pl{};
+    pl.n1 = n1;
+    pl.n2 = n2;
+    if (n2 > 0 && n1 > 0) {
+        pl.per1 = (n1 + kNumXcd - 1) / kNumXcd;
+        int rounds = (pl.per1 + grid / kNumXcd - 1) / (grid / kNumXcd);
+        if (n2 - 2 * (rounds * grid - kNumXcd * pl.per1) > grid) ++rounds;
+        pl.rounds = rounds;
+        pl.cpr = (pl.per1 + rounds - 1) / rounds;
+        pl.full_rounds = pl.per1 / pl.cpr;
+        pl.last_cols = pl.per1 - pl.full_rounds * pl.cpr;
+        pl.slots = rounds * grid - kNumXcd * pl.per1;
+        pl.carried = min(n2, 2 * pl.slots);
+    }
+    pl.rest = ring_phase(n2 > 0 ? n2 - pl.carried : n1, grid, allow_split);
+    pl.virtual_blocks = pl.rounds * grid + pl.rest.blocks + pl.rest.pieces;
+    return pl;
+}
+
+struct RingSlot {
+    int phase;  // 0 / 1 for phase 1 / 2; -1: no tile
+    int tile;   // index inside the phase
+    int piece;  // -1, or 0 / 1 for the two 128-column halves
+};
+
+// Tile `sub` (0 or 1) of virtual workgroup q.
+__device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int q, int sub) {
+    RingSlot s{-1, 0, -1};
+    const int base = pl.rounds * grid;
+    if (q < base) {
+        // Column j of the XCD's slots, rotated by the round so that the
+        // phase-2 slots move to other CUs each round (a CU that always carried
+        // them would fall further behind its XCD's lockstep every round).
+        const int per_xcd = grid / kNumXcd, r = q / grid, pos = q - r * grid;
+        const int j = (pos / kNumXcd + r * (per_xcd - pl.cpr)) % per_xcd;
+        const int cols = r < pl.full_rounds ? pl.cpr : (r == pl.full_rounds ? pl.last_cols : 0);
+        if (j < cols) {
+            const int tile = (pos % kNumXcd) * pl.per1 + r * pl.cpr + j;
+            if (sub == 0 && tile < pl.n1) s = RingSlot{0, tile, -1};
+            return s;
+        }
+        // A phase-2 slot: its index among the rounds' phase-2 slots, in q order.
+        const int per_round = grid - kNumXcd * pl.cpr;
+        int idx = r <= pl.full_rounds
+                      ? r * per_round
+                      : pl.full_rounds * per_round + grid - kNumXcd * pl.last_cols +
+                            (r - pl.full_rounds - 1) * grid;
+        idx += (j - cols) * kNumXcd + pos % kNumXcd;
+        const int lo = static_cast<int>(static_cast<int64_t>(idx) * pl.carried / pl.slots);
+        const int hi = static_cast<int>(static_cast<int64_t>(idx + 1) * pl.carried / pl.slots);
+        if (lo + sub < hi) s = RingSlot{1, lo + sub, -1};
+        return s;
+    }
+    if (sub != 0) return s;
+    const int phase = pl.n2 > 0 ? 1 : 0;
+    const int first = pl.n2 > 0 ? pl.carried : 0;
+    const RingPhase& ph = pl.rest;
+    const int v = q - base;
+    if (v < ph.blocks) {
+        const int per = ph.blocks / kNumXcd;
+        const int tile = (v % kNumXcd) * per + v / kNumXcd;
+        if (tile < ph.main) s = RingSlot{phase, first + tile, -1};
+    } else if (v - ph.blocks < ph.pieces) {
+        const int r = v - ph.blocks;
+        s = RingSlot{phase, first + ph.main + r / 2, r % 2};
+    }
+    return s;
+}
+
+// The fast-path kernel is persistent: one workgroup per CU walks its virtual
+// workgroups and, once a tile's k-loop is done, issues the next tile's first
+// stages before running the epilogue, so their latency hides behind the
+// epilogue's arithmetic and stores, and the per-workgroup start-up is paid
+// once per CU. Tiles are decoded from a per-wave table (lane e = expert e)
+// instead of a loop over the offsets per tile. Measured: C3 and C5 expert
+// GEMMs 5-11% faster, C4 T=4096 about 1%.
 struct RingWork {
     bool valid;
     int expert;
@@ -746,52 +848,24 @@ __device__ __forceinline__ RingTable ring_table(const GemmParams& p) {
     return t;
 }
 
-// Virtual workgroup q -> tile: phase 1 then phase 2, each XCD-contiguous, then
-// each phase's split pieces (see ring_phase).
+// Slot -> tile: expert, rows, columns and ring variant.
 template <bool SWIGLU>
-__device__ __forceinline__ RingWork ring_decode(const GemmParams& p, const RingTable& t, const RingPhase& ph1,
-                                                const RingPhase& ph2, int q) {
+__device__ __forceinline__ RingWork ring_locate(const GemmParams& p, const RingTable& t, const RingSlot& s) {
     RingWork w{false, 0, 0, 0, 0, 0};
-    int phase = -1, tile = 0, piece = -1;
-    if (q < ph1.blocks) {
-        const int per = ph1.blocks / kNumXcd;
-        tile = (q % kNumXcd) * per + q / kNumXcd;
-        if (tile >= ph1.main) return w;
-        phase = 0;
-    } else if (q < ph1.blocks + ph1.pieces) {
-        const int r = q - ph1.blocks;
-        tile = ph1.main + r / 2;
-        piece = r % 2;
-        phase = 0;
-    } else {
-        q -= ph1.blocks + ph1.pieces;
-        if (q < ph2.blocks) {
-            const int per = ph2.blocks / kNumXcd;
-            tile = (q % kNumXcd) * per + q / kNumXcd;
-            if (tile >= ph2.main) return w;
-            phase = 1;
-        } else if (q < ph2.blocks + ph2.pieces) {
-            const int r = q - ph2.blocks;
-            tile = ph2.main + r / 2;
-            piece = r % 2;
-            phase = 1;
-        } else {
-            return w;
-        }
-    }
+    if (s.phase < 0) return w;
     const int lane = threadIdx.x & 63;
-    const int first = phase == 0 ? t.s1 : t.s2;
-    const int count = phase == 0 ? t.c1 : t.c2;
+    const int first = s.phase == 0 ? t.s1 : t.s2;
+    const int count = s.phase == 0 ? t.c1 : t.c2;
     // The tile's expert: the last one (in order) with tiles in this phase starting at or before it.
-    const uint64_t owners = __ballot(lane < p.experts && count > 0 && first <= tile);
+    const uint64_t owners = __ballot(lane < p.experts && count > 0 && first <= s.tile);
     if (owners == 0) return w;
     const int e = 63 - __builtin_clzll(owners);
-    const int rel = tile - __builtin_amdgcn_readlane(first, e);
+    const int rel = s.tile - __builtin_amdgcn_readlane(first, e);
     const int mf = __builtin_amdgcn_readlane(t.mf, e);
     const int span = __builtin_amdgcn_readlane(t.span, e);
     const int off = __builtin_amdgcn_readlane(t.off, e);
     int n_tile, m_tile;
-    if (phase == 0) {
+    if (s.phase == 0) {
         n_tile = rel / mf;
         m_tile = rel - n_tile * mf;
     } else {
@@ -805,10 +879,10 @@ __device__ __forceinline__ RingWork ring_decode(const GemmParams& p, const RingT
     w.variant = rem_rows > 128 ? 0 : (rem_rows > 64 ? 1 : 2);
     if constexpr (SWIGLU) {
         w.col0 = static_cast<int64_t>(n_tile) * 128;
-    } else if (piece < 0) {
+    } else if (s.piece < 0) {
         w.col0 = static_cast<int64_t>(n_tile) * 256;
     } else {
-        w.col0 = static_cast<int64_t>(n_tile) * 256 + piece * 128;
+        w.col0 = static_cast<int64_t>(n_tile) * 256 + s.piece * 128;
         w.variant += 3;
     }
     w.expert = e;
@@ -856,26 +930,27 @@ template <bool SWIGLU>
 __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) char lds[kRingBytes];
     const RingTable table = ring_table(p);
-    const RingPhase ph1 = ring_phase(table.n_full, p.n_cu, !SWIGLU);
-    const RingPhase ph2 = ring_phase(table.n_part, p.n_cu, !SWIGLU);
-    const int virtual_blocks = ph1.blocks + ph1.pieces + ph2.blocks + ph2.pieces;
-    // The next virtual workgroup of this workgroup with work, from q on.
-    auto next = [&](int& q) {
+    const int grid = static_cast<int>(gridDim.x);
+    const RingPlan plan = ring_plan(table.n_full, table.n_part, grid, !SWIGLU);
+    // The next tile of this workgroup at or after tile `sub` of virtual workgroup q.
+    auto next = [&](int& q, int& sub) {
         RingWork w{false, 0, 0, 0, 0, 0};
-        for (; q < virtual_blocks; q += gridDim.x) {
-            w = ring_decode<SWIGLU>(p, table, ph1, ph2, q);
-            if (w.valid) break;
+        for (; q < plan.virtual_blocks; q += grid, sub = 0) {
+            for (; sub < 2; ++sub) {
+                w = ring_locate<SWIGLU>(p, table, ring_slot(plan, grid, q, sub));
+                if (w.valid) return w;
+            }
         }
         return w;
     };
-    int q = blockIdx.x;
-    RingWork cur = next(q);
+    int q = blockIdx.x, sub = 0;
+    RingWork cur = next(q, sub);
     if (!cur.valid) return;
     ring_prologue<SWIGLU>(p, lds, cur);
     bool after_epilogue = false;
     for (;;) {
-        int qn = q + gridDim.x;
-        const RingWork nxt = next(qn);
+        int qn = q, sn = sub + 1;
+        const RingWork nxt = next(qn, sn);
         auto hook = [&] {
             if (!nxt.valid) return;
             // Opaque copies: nothing derived from the next tile may be hoisted
@@ -895,6 +970,7 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
         if (!nxt.valid) break;
         cur = nxt;
         q = qn;
+        sub = sn;
         after_epilogue = true;
     }
 }
@@ -941,6 +1017,13 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_narrow_kernel(GemmP
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
+// Upper bound on the persistent GEMM's workgroups (0: one per CU), process-wide.
+static std::atomic<int> g_gemm_workgroup_limit{0};
+
+void set_gemm_workgroup_limit(int workgroups) {
+    g_gemm_workgroup_limit.store(workgroups, std::memory_order_relaxed);
+}
+
 // Compute units of the current device, cached per device id.
 static int device_cu_count() {
     static int cached[64] = {0};
@@ -963,7 +1046,6 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     const int64_t m_bound = (rows + BM - 1) / BM + p.experts;
     int64_t blocks = m_bound * p.n_tiles;
     if (blocks == 0) return MOE_OK;
-    p.n_cu = device_cu_count();
     if (BM == 256 && BN == 256 && p.k % kStageK == 0 && rows <= 128) {
         GemmParams q = p;
         const int cols = rows <= 64 ? narrow_cols<SWIGLU, 64>() : narrow_cols<SWIGLU, 128>();
@@ -979,14 +1061,16 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
         return check_launch("grouped_gemm_narrow_kernel");
     }
     if (BM == 256 && BN == 256 && p.k % kStageK == 0) {
-        // Two phases, each rounded up to the XCD count, plus room for the split
-        // tail pieces (at most n_cu per phase).
-        int64_t ring_blocks = blocks + 2 * kNumXcd;
-        if (!SWIGLU) ring_blocks += 2 * static_cast<int64_t>(p.n_cu);
-        if (ring_blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
         // One workgroup per CU (the ring fills a CU's LDS), each walking the
-        // virtual workgroups above; row offsets fit 32 bits (checked by the ABI).
-        const int64_t grid = ring_blocks < p.n_cu ? ring_blocks : p.n_cu;
+        // virtual workgroups of the device-side plan, whose XCD ranges need a
+        // multiple of 8 workgroups. Row offsets fit 32 bits (checked by the ABI).
+        if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
+        int64_t grid = device_cu_count();
+        const int limit = g_gemm_workgroup_limit.load(std::memory_order_relaxed);
+        if (limit > 0 && limit < grid) grid = limit;
+        if (blocks < grid) grid = blocks;
+        grid = grid / kNumXcd * kNumXcd;
+        if (grid < kNumXcd) grid = kNumXcd;
         hipLaunchKernelGGL((grouped_gemm_persistent_kernel<SWIGLU>), dim3(static_cast<unsigned>(grid)),
                            dim3(kRingThreads), 0, stream, p);
         return check_launch("grouped_gemm_persistent_kernel");

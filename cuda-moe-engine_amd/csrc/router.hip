@@ -1,6 +1,6 @@
 // Routing kernels for gfx950: bias + top-k (ties to the lower expert id) +
 // selected-score softmax, on given logits or with the fp32 router projection
-// fused in (on MFMA, see router_fused_kernel).
+// fused in (on MFMA, see router_ring_kernel).
 //
 // Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:325-376 (tie rule
 // :331-333, K=2 weight formula :366-374) and src/moe_dispatch/layer.py:122-135.

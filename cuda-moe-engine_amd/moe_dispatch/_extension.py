@@ -225,6 +225,11 @@ class HipExtension:
             gate_up.shape[1] // 2, gate_up.shape[0], _stream(x.device))
         self.lib.check(status, "gateup_swiglu_out")
 
+    def set_gemm_workgroups(self, workgroups):
+        """Bound the persistent grouped GEMM's workgroups (0: one per CU); results do not change."""
+        _check(isinstance(workgroups, int) and workgroups >= 0, "workgroups must be a non-negative int")
+        self.lib.check(self.lib.moe_set_gemm_workgroups(workgroups), "set_gemm_workgroups")
+
     @staticmethod
     def _check_gemm(x, weight, offsets, output, out_cols):
         _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,

@@ -13,7 +13,7 @@ from functools import lru_cache
 from pathlib import Path
 
 LIBRARY_NAME = "libmoe_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -40,6 +40,7 @@ _SIGNATURES = {
     "moe_swiglu": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "moe_grouped_gemm": (_int, [_c_void_p] * 4 + [_i64] * 4 + [_c_void_p]),
     "moe_grouped_gateup_swiglu": (_int, [_c_void_p] * 4 + [_i64] * 4 + [_c_void_p]),
+    "moe_set_gemm_workgroups": (_int, [_i64]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 2
+#define MOE_ABI_VERSION 3
 
 typedef enum {
     MOE_DTYPE_F32 = 0,
@@ -158,6 +158,18 @@ int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offse
 int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
                               const int32_t* offsets, int64_t rows, int64_t hidden,
                               int64_t intermediate, int64_t experts, void* stream);
+
+/*
+ * Upper bound on the workgroups of the persistent grouped GEMM (both
+ * moe_grouped_gemm and moe_grouped_gateup_swiglu): 0 (the default) runs one
+ * per CU; n > 0 runs min(n, CUs), rounded down to a multiple of 8 (at least 8).
+ * Process-wide; it takes effect at the next launch. Scheduling only: every
+ * output tile is computed by one workgroup with the same MFMA chain, so
+ * results are identical for every value. For callers that leave CUs to
+ * concurrent work on other streams, and for tests of the schedule. No
+ * counterpart in the reference (its GEMM is torch's grouped_mm).
+ */
+int moe_set_gemm_workgroups(int64_t workgroups);
 
 #ifdef __cplusplus
 }

@@ -68,6 +68,10 @@ def test_validation_errors_without_launching():
     assert lib.moe_router_scratch_bytes(65, 64) == -1
     assert lib.moe_router_fused(16, 16, 16, 16, 16, 16, None, 16, 3 * 8 * 64 * 2 - 1, 4, 64, 8, 2, None) == 4
     assert b"router scratch needs" in lib.moe_last_error()
+    # The persistent GEMM's workgroup bound (scheduling only; no launch here).
+    assert lib.moe_set_gemm_workgroups(-1) == 1
+    assert lib.moe_set_gemm_workgroups(1 << 40) == 1
+    assert lib.moe_set_gemm_workgroups(16) == 0 and lib.moe_set_gemm_workgroups(0) == 0
 
 
 def test_error_surfaces_as_runtime_error():

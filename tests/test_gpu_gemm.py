@@ -74,6 +74,57 @@ def test_grouped_gemm_matches_float64(ext, counts, alignment, n, k):
     assert np.all(got[used:] == 7.0), "rows past offsets[E] must not be written"
 
 
+SCHEDULE_CASES = [
+    # counts, alignment, output columns (N, or I for gate/up), k, gate/up?, workgroup bounds.
+    # With 8-40 workgroups these small launches take every path of the persistent plan:
+    # slots carrying two short tiles, an extra round, leftovers after the rounds, split
+    # pieces, a partial last round (tests/test_ring_plan.py checks which case reaches which).
+    ([300, 700, 3, 260, 40, 1, 129, 520], 8, 512, 128, False, (8, 24)),
+    ([300, 700, 3, 260, 40, 1, 129, 520], 8, 512, 128, True, (8, 16, 40)),
+    ([1030, 20, 5, 257, 64, 600, 0, 90], 8, 1024, 192, False, (8, 16, 40)),
+    ([1030, 20, 5, 257, 64, 600, 0, 90], 8, 640, 64, True, (8, 16, 24)),
+    ([512, 256], 8, 1024, 128, False, (8,)),
+]
+
+
+@pytest.mark.parametrize("counts,alignment,n,k,swiglu,grids", SCHEDULE_CASES)
+def test_schedule_does_not_change_results(ext, counts, alignment, n, k, swiglu, grids):
+    """Every tile is written, and by the same MFMA chain, whatever the persistent grid."""
+    experts = len(counts)
+    a, offsets, rows = _inputs(counts, alignment, k, seed=n + 3 * k)
+    w = (torch.randn(experts, 2 * n if swiglu else n, k, device="cuda") / k**0.5).bfloat16()
+    run = ext.gateup_swiglu_out if swiglu else ext.grouped_gemm_out
+
+    def once():
+        out = torch.full((rows, n), 5.0, device="cuda").bfloat16()
+        run(a, w, offsets, out)
+        torch.cuda.synchronize()
+        return out
+
+    try:
+        ext.set_gemm_workgroups(0)
+        default = once()
+        for grid in grids:
+            ext.set_gemm_workgroups(grid)
+            assert torch.equal(once(), default), f"{grid} workgroups changed the output"
+    finally:
+        ext.set_gemm_workgroups(0)
+    off = to_np(offsets)
+    used = int(off[-1])
+    got = to_np(default)
+    assert np.all(got[used:] == 5.0), "rows past offsets[E] must not be written"
+    ref = np.zeros((used, n), dtype=np.float32)
+    for e in range(experts):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi > lo:
+            proj = (a[lo:hi].float() @ w[e].float().t())
+            if swiglu:
+                g, u = proj[:, :n].bfloat16().float(), proj[:, n:].bfloat16().float()
+                proj = torch.nn.functional.silu(g) * u
+            ref[lo:hi] = to_np(proj)
+    assert rel_l2(got[:used], ref) < 3e-3
+
+
 GATEUP_CASES = [
     # counts, alignment, hidden, intermediate
     ([5, 0, 37, 300, 8, 0, 1, 64], 8, 64, 128),

@@ -1,0 +1,189 @@
+"""The persistent grouped GEMM's tile plan, restated and checked on the CPU.
+
+grouped_gemm_persistent_kernel (cuda-moe-engine_amd/csrc/gemm.hip: ring_plan,
+ring_slot) walks virtual workgroups q = blockIdx.x + i*G in rounds of G. Full
+row tiles (phase 1) run in 8 XCD-contiguous ranges, cpr per XCD and round;
+the other slots of the rounds carry one or two of the experts' short last row
+tiles (phase 2); phase-2 tiles the rounds do not take, or phase 1 when there is
+no phase 2, run after the rounds with an optional split of a short last round
+into 128-column pieces (plain GEMM only). This restates those formulas and
+checks that every tile (or both halves of a split tile) is assigned exactly
+once for random expert layouts and grid sizes, that the rounds keep each XCD's
+phase-1 tiles in order, and that the measured shapes get the intended plans.
+The GPU test tests/test_gpu_gemm.py::test_schedule_does_not_change_results runs
+the kernel itself at the grid sizes used here.
+"""
+
+import random
+
+import pytest
+
+XCD = 8
+
+
+def phase_counts(counts, alignment, n_tiles):
+    spans = [(c + alignment - 1) // alignment * alignment for c in counts]
+    mf = [s // 256 + (1 if s % 256 > 128 else 0) for s in spans]
+    n1 = sum(m * n_tiles for m in mf)
+    n2 = sum(((s + 255) // 256 - m) * n_tiles for s, m in zip(spans, mf))
+    return n1, n2
+
+
+def ring_phase(count, grid, allow_split):
+    rem = count % grid
+    split = allow_split and rem > 0 and 2 * rem <= grid
+    main = count - rem if split else count
+    return {"main": main, "blocks": (main + XCD - 1) // XCD * XCD, "pieces": 2 * rem if split else 0}
+
+
+def ring_plan(n1, n2, grid, allow_split):
+    pl = {"n1": n1, "n2": n2, "per1": 0, "cpr": 0, "rounds": 0, "full_rounds": 0, "last_cols": 0,
+          "slots": 0, "carried": 0}
+    if n2 > 0 and n1 > 0:
+        per1 = (n1 + XCD - 1) // XCD
+        rounds = (per1 + grid // XCD - 1) // (grid // XCD)
+        if n2 - 2 * (rounds * grid - XCD * per1) > grid:
+            rounds += 1
+        cpr = (per1 + rounds - 1) // rounds
+        slots = rounds * grid - XCD * per1
+        pl.update(per1=per1, rounds=rounds, cpr=cpr, full_rounds=per1 // cpr,
+                  last_cols=per1 - (per1 // cpr) * cpr, slots=slots, carried=min(n2, 2 * slots))
+    pl["rest"] = ring_phase(n2 - pl["carried"] if n2 > 0 else n1, grid, allow_split)
+    pl["virtual_blocks"] = pl["rounds"] * grid + pl["rest"]["blocks"] + pl["rest"]["pieces"]
+    return pl
+
+
+def ring_slot(pl, grid, q, sub):
+    """(phase, tile, piece) of tile `sub` of virtual workgroup q, or None."""
+    base = pl["rounds"] * grid
+    if q < base:
+        r, pos = divmod(q, grid)
+        per_xcd = grid // XCD
+        j = (pos // XCD + r * (per_xcd - pl["cpr"])) % per_xcd  # rotated per round
+        cols = pl["cpr"] if r < pl["full_rounds"] else (pl["last_cols"] if r == pl["full_rounds"] else 0)
+        if j < cols:
+            tile = (pos % XCD) * pl["per1"] + r * pl["cpr"] + j
+            return (0, tile, -1) if sub == 0 and tile < pl["n1"] else None
+        per_round = grid - XCD * pl["cpr"]
+        if r <= pl["full_rounds"]:
+            idx = r * per_round
+        else:
+            idx = pl["full_rounds"] * per_round + grid - XCD * pl["last_cols"] + (r - pl["full_rounds"] - 1) * grid
+        idx += (j - cols) * XCD + pos % XCD
+        lo = idx * pl["carried"] // pl["slots"]
+        hi = (idx + 1) * pl["carried"] // pl["slots"]
+        return (1, lo + sub, -1) if lo + sub < hi else None
+    if sub:
+        return None
+    phase = 1 if pl["n2"] > 0 else 0
+    first = pl["carried"] if pl["n2"] > 0 else 0
+    rest, v = pl["rest"], q - base
+    if v < rest["blocks"]:
+        per = rest["blocks"] // XCD
+        tile = (v % XCD) * per + v // XCD
+        return (phase, first + tile, -1) if tile < rest["main"] else None
+    if v - rest["blocks"] < rest["pieces"]:
+        r = v - rest["blocks"]
+        return (phase, first + rest["main"] + r // 2, r % 2)
+    return None
+
+
+def walk(n1, n2, grid, allow_split):
+    """Per workgroup, the (phase, tile, piece) sequence it runs."""
+    pl = ring_plan(n1, n2, grid, allow_split)
+    runs = []
+    for wg in range(grid):
+        seq = []
+        for q in range(wg, pl["virtual_blocks"], grid):
+            for sub in (0, 1):
+                s = ring_slot(pl, grid, q, sub)
+                if s is not None:
+                    seq.append((q, s))
+        runs.append(seq)
+    return pl, runs
+
+
+def check_cover(n1, n2, grid, allow_split):
+    pl, runs = walk(n1, n2, grid, allow_split)
+    seen = {}
+    for seq in runs:
+        for _, (phase, tile, piece) in seq:
+            key = (phase, tile, piece)
+            assert key not in seen, f"tile {key} assigned twice"
+            seen[key] = True
+    parts = {}
+    for phase, tile, piece in seen:
+        parts.setdefault((phase, tile), set()).add(piece)
+    assert set(parts) == {(0, t) for t in range(n1)} | {(1, t) for t in range(n2)}
+    assert all(p in ({-1}, {0, 1}) for p in parts.values())
+    assert not (pl["carried"] and not allow_split and pl["rest"]["pieces"])
+    # In the rounds, the workgroups of XCD x (those with blockIdx % 8 == x) run
+    # exactly phase-1 range x, each round's tiles before the next round's.
+    for x in range(XCD):
+        ranged = sorted((q // grid, s[1]) for seq in runs[x::XCD] for q, s in seq
+                        if s[0] == 0 and q < pl["rounds"] * grid)
+        first = x * pl["per1"]
+        assert [t for _, t in ranged] == list(range(first, min(first + pl["per1"], n1)))
+    return pl, runs
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_every_tile_runs_once(seed):
+    rng = random.Random(seed)
+    for _ in range(120):
+        experts = rng.randint(1, 64)
+        counts = [rng.choice([0, rng.randint(1, 40), rng.randint(0, 600), rng.randint(0, 3000)])
+                  for _ in range(experts)]
+        n1, n2 = phase_counts(counts, rng.choice([1, 8]), rng.randint(1, 40))
+        check_cover(n1, n2, rng.choice([8, 16, 24, 64, 256]), rng.random() < 0.5)
+
+
+def test_grid_sizes_used_on_the_gpu_cover_each_path():
+    """The GPU schedule test's cases reach the two-tile slots, leftovers and split pieces."""
+    from tests.test_gpu_gemm import SCHEDULE_CASES
+
+    reached = set()
+    for counts, alignment, n, k, swiglu, grids in SCHEDULE_CASES:
+        n_tiles = -(-n // (128 if swiglu else 256))
+        n1, n2 = phase_counts(counts, alignment, n_tiles)
+        for grid in grids:
+            pl, runs = check_cover(n1, n2, grid, not swiglu)
+            per_q = {}
+            for seq in runs:
+                for q, _ in seq:
+                    per_q[q] = per_q.get(q, 0) + 1
+            if max(per_q.values(), default=0) == 2:
+                reached.add("two tiles in a slot")
+            if pl["carried"] and pl["carried"] < n2:
+                reached.add("leftover after the rounds")
+            if pl["rest"]["pieces"]:
+                reached.add("pieces")
+            if pl["rounds"] and pl["last_cols"]:
+                reached.add("partial last round")
+            if pl["rounds"] > (pl["per1"] + grid // XCD - 1) // (grid // XCD):
+                reached.add("extra round")
+    assert reached == {"two tiles in a slot", "leftover after the rounds", "pieces", "partial last round",
+                       "extra round"}
+
+
+def test_phase2_slots_rotate_over_the_cus():
+    # 14 rounds of 30 phase-1 columns per XCD: each workgroup carries short tiles in at most one round.
+    c4 = [1040, 1095, 1010, 1026, 1019, 1025, 1003, 974]
+    pl, runs = check_cover(*phase_counts(c4, 8, 112), 256, False)
+    rounds_carrying = [len({q for q, s in seq if s[0] == 1}) for seq in runs]
+    assert max(rounds_carrying) == 1 and sum(rounds_carrying) == pl["slots"] == 256
+
+
+def test_measured_shapes_get_the_intended_plans():
+    # H=4096, I=14336, E=8, 4096 tokens (counts from the bench): 14 rounds of phase 1
+    # alone would leave 448 short tiles for the end; one more round carries them all.
+    c4 = [1040, 1095, 1010, 1026, 1019, 1025, 1003, 974]
+    pl = ring_plan(*phase_counts(c4, 8, 112), 256, False)
+    assert (pl["rounds"], pl["cpr"], pl["carried"], pl["n2"]) == (15, 30, 448, 448)
+    # Its down GEMM (512 full tiles = 2 rounds, 64 short tiles): no extra round;
+    # the short tiles run last as 128 split pieces.
+    pl = ring_plan(*phase_counts(c4, 8, 16), 256, True)
+    assert (pl["rounds"], pl["carried"], pl["rest"]["pieces"]) == (2, 0, 128)
+    # No short tiles: phase 1 alone, as before.
+    pl = ring_plan(*phase_counts([1024] * 8, 8, 112), 256, False)
+    assert (pl["rounds"], pl["rest"]["blocks"]) == (0, 3584)
