@@ -198,7 +198,7 @@ def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, 
     """
     active = int((counts > 0).sum())
     byte = 2.0 * (active * 2 * inter * hidden + n_assign * hidden + n_assign * inter)
-    kernel = "grouped_gemm_narrow_kernel<true>" if packed_rows <= 128 else "grouped_gemm_persistent_kernel<true>"
+    kernel = "grouped_gemm_decode_kernel<true>" if packed_rows <= 128 else "grouped_gemm_persistent_kernel<true>"
     entry = {"kernel": kernel + " (gate/up GEMM + SwiGLU epilogue)"}
     if flop / byte < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
         achieved = byte / (launch_us * 1e-6) / 1e9

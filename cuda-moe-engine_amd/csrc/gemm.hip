@@ -305,18 +305,18 @@ constexpr uint32_t kRingBytes = 160 * 1024;    // all of a gfx950 CU's LDS
 // 4): small tiles compute a stage in a few hundred cycles, so A needs the same
 // lead as B. Otherwise (the 256 x 256 tile) A gets two stages and B as many as
 // fit beside them.
-constexpr int ring_equal_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
+constexpr int ring_equal_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes, int cap = 4) {
     const int fit = static_cast<int>(bytes / (a_stage + b_stage));
-    return fit < 4 ? fit : 4;
+    return fit < cap ? fit : cap;
 }
-constexpr int ring_b_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
-    if (ring_equal_stages(a_stage, b_stage, bytes) >= 3) return ring_equal_stages(a_stage, b_stage, bytes);
+constexpr int ring_b_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes, int cap = 4) {
+    if (ring_equal_stages(a_stage, b_stage, bytes, cap) >= 3) return ring_equal_stages(a_stage, b_stage, bytes, cap);
     const int fit = bytes < 2 * a_stage ? 0 : static_cast<int>((bytes - 2 * a_stage) / b_stage);
-    return fit < 4 ? fit : 4;
+    return fit < cap ? fit : cap;
 }
-constexpr int ring_a_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes) {
-    if (ring_equal_stages(a_stage, b_stage, bytes) >= 3) return ring_equal_stages(a_stage, b_stage, bytes);
-    const int sb = ring_b_stages(a_stage, b_stage, bytes);
+constexpr int ring_a_stages(uint32_t a_stage, uint32_t b_stage, uint32_t bytes, int cap = 4) {
+    if (ring_equal_stages(a_stage, b_stage, bytes, cap) >= 3) return ring_equal_stages(a_stage, b_stage, bytes, cap);
+    const int sb = ring_b_stages(a_stage, b_stage, bytes, cap);
     const int fit = static_cast<int>((bytes - sb * b_stage) / a_stage);
     return fit < sb ? fit : sb;
 }
@@ -330,19 +330,11 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
     return (g * u) * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// One output tile on v_mfma_f32_16x16x32_bf16: rows [row0, row0 + SMT*64) of one
-// expert (clamped to row_end) by BNT weight rows starting at output column
-// col0, with a ring in the first LDS_BYTES of `lds`. A 64-k stage is two 32-k
-// sub-steps; in each, every wave multiplies its (WTM/16) x (WTN/16) grid of
-// 16x16 blocks with one MFMA each while it reads the fragments of the next
-// sub-step. The 16x16x32 form sustains a higher clock than 32x32x16 under the
-// power limit (measured on MI355X: 1.91 vs 1.66 GHz with the same read and
-// load mix), so it moves the same FLOPs about 10% faster.
 // The ring's shape and direct-to-LDS loads for one tile: rows [row0,
 // row0 + SMT*64) of one expert (clamped to row_end) by BNT weight rows from
-// output column col0, in the first LDS_BYTES of `lds`. The four waves split
-// the tile as (4/WC) row blocks x WC column blocks.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2>
+// output column col0, in the first LDS_BYTES of `lds`, at most MAXS stages
+// deep. The four waves split the tile as (4/WC) row blocks x WC column blocks.
+template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2, int MAXS = 4>
 struct RingOps {
     static constexpr int WAVES = kRingThreads / kWave;
     static constexpr int TM = SMT * 64;
@@ -355,8 +347,8 @@ struct RingOps {
     static constexpr int LOADS = A_LOADS + B_LOADS;
     static constexpr uint32_t A_STAGE = TM * kRowBytes;   // bytes of one stage of A
     static constexpr uint32_t B_STAGE = BNT * kRowBytes;  // bytes of one stage of B
-    static constexpr int SB = ring_b_stages(A_STAGE, B_STAGE, LDS_BYTES);
-    static constexpr int SA = ring_a_stages(A_STAGE, B_STAGE, LDS_BYTES);
+    static constexpr int SB = ring_b_stages(A_STAGE, B_STAGE, LDS_BYTES, MAXS);
+    static constexpr int SA = ring_a_stages(A_STAGE, B_STAGE, LDS_BYTES, MAXS);
     static constexpr uint32_t B_BASE = SA * A_STAGE;      // B stages follow the A stages
     static constexpr uint32_t FRAG = 16 * kRowBytes;      // bytes between 16-row fragments
     static_assert(A_LOADS >= 1 && B_LOADS >= 1 && FA >= 1 && FB >= 2, "tile shape");
@@ -442,6 +434,13 @@ struct NoHook {
     __device__ void operator()() const {}
 };
 
+// One output tile on v_mfma_f32_16x16x32_bf16 (shape as in RingOps). A 64-k
+// stage is two 32-k sub-steps; in each, every wave multiplies its (WTM/16) x
+// (WTN/16) grid of 16x16 blocks with one MFMA each while it reads the
+// fragments of the next sub-step. The 16x16x32 form sustains a higher clock
+// than 32x32x16 under the power limit (measured on MI355X: 1.91 vs 1.66 GHz
+// with the same read and load mix), so it moves the same FLOPs about 10%
+// faster.
 //
 // own_prologue: issue the prologue loads here (else a previous call's hook
 // issued them). wait_all: a previous epilogue's stores may be in flight, and
@@ -449,11 +448,11 @@ struct NoHook {
 // before the first read instead of counting loads. hook: runs once the
 // k-loop is done and every wave has finished with the ring (it may refill
 // LDS), before the epilogue.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2>
+template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end, bool own_prologue = true,
                                           bool wait_all = false, const Hook& hook = Hook{}) {
-    using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC>;
+    using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC, MAXS>;
     constexpr int WTM = R::WTM, WTN = R::WTN, FA = R::FA, FB = R::FB;
     constexpr int A_LOADS = R::A_LOADS, B_LOADS = R::B_LOADS;
     constexpr int SA = R::SA, SB = R::SB;
@@ -975,43 +974,127 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
     }
 }
 
-// Decode-sized launches (at most 128 rows in all): every expert has at most one
-// row tile, so the work is streaming the active experts' weights. Tiles are
-// narrow so that a single token's two experts still spread over the CUs: 64
-// activation columns (128 weight rows, waves 2 x 2) for the gate/up GEMM, 64
-// output columns for the down GEMM, and 32 (waves 4 x 1) when at most 64 rows
-// are packed (measured at T=1: down 54.7 -> 51.8 us; at T=16 the 4 x 1 waves,
-// which all read every B fragment, ran 7% slower than 64 columns). Each output
-// is the same MFMA chain in k order as on the wide path. MAX_ROWS (64 or 128)
-// bounds every expert's span; the 64-row instance needs less LDS, so more
-// blocks share a CU.
+// Decode-sized launches (at most 128 packed rows in all): every expert has at
+// most one row tile, so the work is streaming the active experts' weights (at
+// T=1, 2 x 235 MB for the gate/up GEMM). The kernel is persistent like the
+// wide one: one workgroup per CU walks the tiles (active expert by active
+// expert, column tile fastest) and issues the next tile's first stages before
+// the current tile's epilogue. Tiles are narrow so that a single token's two
+// experts still spread over the CUs: 64 activation columns (128 weight rows,
+// waves 2 x 2) for the gate/up GEMM, 64 output columns for the down GEMM, and
+// 32 (waves 4 x 1) when at most 64 rows are packed (at T=16 the 4 x 1 waves,
+// which all read every B fragment, ran 7% slower than 64 columns). Their
+// stages are small (12-32 KiB), so the ring holds up to eight: a CU has to
+// keep about 32 KiB of loads in flight to stream at the HBM rate (a plain
+// read kernel reaches 6.3-6.4 TB/s with 32 KiB per CU, 5.2 TB/s with 16 KiB).
+// The 64-row gate/up instance is the exception: it keeps three stages (72
+// KiB) so that two workgroups share a CU, which suits a token's 448 tiles
+// better than one workgroup per CU with a deeper ring (T=1: 93 vs 97 us).
+// Each output is the same MFMA chain in k order as on the wide path. MAX_ROWS
+// (64 or 128) bounds every expert's span; a span of at most 64 rows runs the
+// 64-row tile.
 template <bool SWIGLU, int MAX_ROWS>
 constexpr int narrow_cols() { return SWIGLU || MAX_ROWS == 128 ? 64 : 32; }
 
+constexpr int kDecodeStages = 8;
+
 template <bool SWIGLU, int MAX_ROWS>
-__global__ __launch_bounds__(kRingThreads) void grouped_gemm_narrow_kernel(GemmParams p) {
+constexpr uint32_t decode_lds_bytes() {
+    return SWIGLU && MAX_ROWS == 64 ? 3 * (64 + 2 * narrow_cols<SWIGLU, MAX_ROWS>()) * kRowBytes : kRingBytes;
+}
+
+template <bool SWIGLU, int MAX_ROWS>
+__global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmParams p) {
     constexpr int COLS = narrow_cols<SWIGLU, MAX_ROWS>();
     constexpr int BNT = SWIGLU ? 2 * COLS : COLS;
     constexpr int WC = BNT == 32 ? 1 : 2;
-    constexpr uint32_t kLds = 3 * (MAX_ROWS + BNT) * kRowBytes;  // three stages of the largest tile
-    static_assert(MAX_ROWS == 64 || MAX_ROWS == 128, "narrow row tiles");
-    static_assert(ring_a_stages(MAX_ROWS * kRowBytes, BNT * kRowBytes, kLds) >= 2, "narrow ring");
+    constexpr uint32_t kLds = decode_lds_bytes<SWIGLU, MAX_ROWS>();
+    static_assert(MAX_ROWS == 64 || MAX_ROWS == 128, "decode row tiles");
     __shared__ __attribute__((aligned(1024))) char lds[kLds];
-    const int expert = blockIdx.x / p.n_tiles;
-    const int n_tile = blockIdx.x - expert * p.n_tiles;
-    if (expert >= p.experts) return;
-    const int64_t row0 = p.offsets[expert];
-    const int64_t row_end = min(static_cast<int64_t>(p.offsets[expert + 1]), p.rows);
-    if (row0 < 0 || row0 >= row_end) return;
-    const int64_t span = row_end - row0;  // <= p.rows <= MAX_ROWS (checked by the launcher)
-    const int64_t col0 = static_cast<int64_t>(n_tile) * COLS;
-    if constexpr (MAX_ROWS == 128) {
-        if (span > 64) {
-            ring_tile<2, BNT, SWIGLU, kLds, NoHook, WC>(p, lds, expert, col0, row0, row_end);
-            return;
-        }
+    const int lane = threadIdx.x & 63;
+    int off = 0, span = 0;
+    if (lane < p.experts) {
+        off = p.offsets[lane];
+        span = max(p.offsets[lane + 1] - off, 0);
     }
-    ring_tile<1, BNT, SWIGLU, kLds, NoHook, WC>(p, lds, expert, col0, row0, row_end);
+    const uint64_t active = __ballot(span > 0);
+    const int rank = __popcll(active & ((uint64_t{1} << lane) - 1));  // active experts before this lane's
+    const int tiles = __popcll(active) * p.n_tiles;
+    const int k_steps = static_cast<int>(p.k / kStageK);
+    struct Work {
+        bool valid;
+        int tall, expert, row0, row_end, col0;  // tall: more than 64 rows
+    };
+    // Tile t: column tile t % n_tiles of the (t / n_tiles)-th active expert.
+    auto locate = [&](int t) {
+        Work w{false, 0, 0, 0, 0, 0};
+        if (t >= tiles) return w;
+        const int k = t / p.n_tiles;
+        const uint64_t owner = __ballot(((active >> lane) & 1) != 0 && rank == k);
+        if (owner == 0) return w;
+        const int e = __builtin_ctzll(owner);
+        const int row0 = __builtin_amdgcn_readlane(off, e);
+        const int rows = __builtin_amdgcn_readlane(span, e);  // <= p.rows <= MAX_ROWS (checked by the launcher)
+        w.row0 = row0;
+        w.row_end = static_cast<int>(min(static_cast<int64_t>(row0) + rows, p.rows));
+        if (w.row0 < 0 || w.row0 >= w.row_end) return w;
+        w.tall = MAX_ROWS == 128 && w.row_end - w.row0 > 64;
+        w.expert = e;
+        w.col0 = (t - k * p.n_tiles) * COLS;
+        w.valid = true;
+        return w;
+    };
+    auto prologue = [&](const Work& w) {
+        if constexpr (MAX_ROWS == 128) {
+            if (w.tall) {
+                RingOps<2, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
+                    .prologue(k_steps);
+                return;
+            }
+        }
+        RingOps<1, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
+            .prologue(k_steps);
+    };
+    auto run = [&](const Work& w, bool wait_all, const auto& hook) {
+        using Hook = std::decay_t<decltype(hook)>;
+        if constexpr (MAX_ROWS == 128) {
+            if (w.tall) {
+                ring_tile<2, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0,
+                                                                                w.row_end, false, wait_all, hook);
+                return;
+            }
+        }
+        ring_tile<1, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end,
+                                                                        false, wait_all, hook);
+    };
+    int t = blockIdx.x;
+    Work cur = locate(t);
+    if (!cur.valid) return;
+    prologue(cur);
+    bool after_epilogue = false;
+    for (;;) {
+        const int tn = t + static_cast<int>(gridDim.x);
+        const Work nxt = locate(tn);
+        auto hook = [&] {
+            if (!nxt.valid) return;
+            // Opaque copies, as in the wide kernel: nothing derived from the
+            // next tile is hoisted into the current tile's k-loop. (The values
+            // are uniform; they go back to scalar registers after the asm.)
+            Work w = nxt;
+            asm volatile("" : "+v"(w.tall), "+v"(w.expert), "+v"(w.row0), "+v"(w.row_end), "+v"(w.col0));
+            w.tall = __builtin_amdgcn_readfirstlane(w.tall);
+            w.expert = __builtin_amdgcn_readfirstlane(w.expert);
+            w.row0 = __builtin_amdgcn_readfirstlane(w.row0);
+            w.row_end = __builtin_amdgcn_readfirstlane(w.row_end);
+            w.col0 = __builtin_amdgcn_readfirstlane(w.col0);
+            prologue(w);
+        };
+        run(cur, after_epilogue, hook);
+        if (!nxt.valid) break;
+        cur = nxt;
+        t = tn;
+        after_epilogue = true;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1050,15 +1133,19 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
         GemmParams q = p;
         const int cols = rows <= 64 ? narrow_cols<SWIGLU, 64>() : narrow_cols<SWIGLU, 128>();
         q.n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
-        const int64_t narrow_blocks = static_cast<int64_t>(p.experts) * q.n_tiles;
-        if (narrow_blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
+        const int64_t tiles = static_cast<int64_t>(p.experts) * q.n_tiles;
+        if (tiles > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
+        // As many workgroups as fit the CUs' LDS, at most one per tile.
+        const uint32_t lds = rows <= 64 ? decode_lds_bytes<SWIGLU, 64>() : decode_lds_bytes<SWIGLU, 128>();
+        int64_t grid = static_cast<int64_t>(device_cu_count()) * (kRingBytes / lds);
+        if (tiles < grid) grid = tiles;
         if (rows <= 64)
-            hipLaunchKernelGGL((grouped_gemm_narrow_kernel<SWIGLU, 64>), dim3(static_cast<unsigned>(narrow_blocks)),
+            hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 64>), dim3(static_cast<unsigned>(grid)),
                                dim3(kRingThreads), 0, stream, q);
         else
-            hipLaunchKernelGGL((grouped_gemm_narrow_kernel<SWIGLU, 128>), dim3(static_cast<unsigned>(narrow_blocks)),
+            hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 128>), dim3(static_cast<unsigned>(grid)),
                                dim3(kRingThreads), 0, stream, q);
-        return check_launch("grouped_gemm_narrow_kernel");
+        return check_launch("grouped_gemm_decode_kernel");
     }
     if (BM == 256 && BN == 256 && p.k % kStageK == 0) {
         // One workgroup per CU (the ring fills a CU's LDS), each walking the

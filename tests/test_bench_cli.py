@@ -50,7 +50,7 @@ def test_gateup_roofline_picks_the_bound_by_intensity():
     dec = bench.gateup_roofline("none", np.array([1, 0, 0, 0, 0, 1, 0, 0]), 58, h, i, 2, 4.0 * 2 * h * i, 100.0)
     weights = 2 * 2 * (2 * i * h)
     assert dec["bound"] == "hbm" and dec["unit"] == "GB/s" and dec["peak"] == bench.HBM_PEAK_GBS
-    assert dec["kernel"].startswith("grouped_gemm_narrow_kernel<true>")
+    assert dec["kernel"].startswith("grouped_gemm_decode_kernel<true>")
     assert weights < dec["bytes_per_launch"] < weights * 1.001
     assert abs(dec["achieved"] - dec["bytes_per_launch"] / 100e-6 / 1e9) < 0.1
     # Prefill: 8192 assignments over 8 experts is far past the ridge point.

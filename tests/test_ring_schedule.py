@@ -11,6 +11,8 @@ instantiate and checks that each wait covers both matrices of the stage it
 guards and that no refill lands in a slot a still-unread stage occupies. The
 depth and wait formulas below are the kernel's; a wrong count (e.g. treating the
 A loads as the newest when SA == SB) fails here for the affected shapes.
+The wide tiles cap the ring at 4 stages; the decode kernel's small stages go
+up to 8.
 """
 
 import itertools
@@ -21,27 +23,27 @@ KIB = 1024
 ROW_BYTES = 128  # one 64-k stage of one row
 
 
-def equal_stages(a_stage, b_stage, lds):
-    return min(lds // (a_stage + b_stage), 4)
+def equal_stages(a_stage, b_stage, lds, cap):
+    return min(lds // (a_stage + b_stage), cap)
 
 
-def b_stages(a_stage, b_stage, lds):
-    if equal_stages(a_stage, b_stage, lds) >= 3:
-        return equal_stages(a_stage, b_stage, lds)
+def b_stages(a_stage, b_stage, lds, cap):
+    if equal_stages(a_stage, b_stage, lds, cap) >= 3:
+        return equal_stages(a_stage, b_stage, lds, cap)
     fit = 0 if lds < 2 * a_stage else (lds - 2 * a_stage) // b_stage
-    return min(fit, 4)
+    return min(fit, cap)
 
 
-def a_stages(a_stage, b_stage, lds):
-    if equal_stages(a_stage, b_stage, lds) >= 3:
-        return equal_stages(a_stage, b_stage, lds)
-    sb = b_stages(a_stage, b_stage, lds)
+def a_stages(a_stage, b_stage, lds, cap):
+    if equal_stages(a_stage, b_stage, lds, cap) >= 3:
+        return equal_stages(a_stage, b_stage, lds, cap)
+    sb = b_stages(a_stage, b_stage, lds, cap)
     return min((lds - sb * b_stage) // a_stage, sb)
 
 
-def replay(tm, bnt, lds, k_steps):
+def replay(tm, bnt, lds, k_steps, cap=4):
     a_stage, b_stage = tm * ROW_BYTES, bnt * ROW_BYTES
-    sb, sa = b_stages(a_stage, b_stage, lds), a_stages(a_stage, b_stage, lds)
+    sb, sa = b_stages(a_stage, b_stage, lds, cap), a_stages(a_stage, b_stage, lds, cap)
     a_loads, b_loads = tm // 32, bnt // 32  # 8 rows per load, four waves
     loads = a_loads + b_loads
     vm_steady = (b_loads if sb > sa else 0) + (sa - 2) * loads
@@ -76,17 +78,26 @@ def replay(tm, bnt, lds, k_steps):
 
 
 def _shapes():
-    shapes = {(tm, bnt, 160 * KIB) for tm, bnt in itertools.product((64, 128, 256), (128, 256))}
-    for max_rows, bnt in ((64, 32), (128, 64), (64, 128), (128, 128)):  # decode tiles (down, gate/up)
-        lds = 3 * (max_rows + bnt) * ROW_BYTES
-        shapes |= {(64, bnt, lds), (max_rows, bnt, lds)}
+    # Wide tiles: at most 4 stages in 160 KiB.
+    shapes = {(tm, bnt, 160 * KIB, 4) for tm, bnt in itertools.product((64, 128, 256), (128, 256))}
+    # Decode tiles (grouped_gemm_decode_kernel): at most 8 stages in 160 KiB.
+    for max_rows, bnt in ((64, 32), (128, 64), (128, 128)):  # down at 64 and 128 rows, gate/up at 128
+        shapes |= {(64, bnt, 160 * KIB, 8), (max_rows, bnt, 160 * KIB, 8)}
+    shapes.add((64, 128, 3 * (64 + 128) * ROW_BYTES, 8))  # gate/up at 64 rows: three stages, two per CU
     return sorted(shapes)
 
 
-@pytest.mark.parametrize("tm,bnt,lds", _shapes())
-def test_ring_waits_cover_each_stage(tm, bnt, lds):
-    for k_steps in (1, 2, 3, 4, 5, 7, 64, 224):
-        replay(tm, bnt, lds, k_steps)
+@pytest.mark.parametrize("tm,bnt,lds,cap", _shapes())
+def test_ring_waits_cover_each_stage(tm, bnt, lds, cap):
+    for k_steps in (1, 2, 3, 4, 5, 7, 9, 64, 224):
+        replay(tm, bnt, lds, k_steps, cap)
+
+
+def test_decode_rings_keep_32_kib_of_weights_in_flight():
+    # Stages in flight while one is read: SB - 1 of B.
+    for tm, bnt in ((64, 32), (64, 64), (128, 64), (128, 128)):
+        sa, sb = replay(tm, bnt, 160 * KIB, 64, cap=8)
+        assert (sb - 1) * bnt * ROW_BYTES >= 28 * KIB, (tm, bnt, sa, sb)
 
 
 def test_full_tile_uses_all_lds_as_two_a_and_three_b_stages():
@@ -96,3 +107,4 @@ def test_full_tile_uses_all_lds_as_two_a_and_three_b_stages():
 def test_small_tiles_get_equal_depths():
     assert replay(64, 64, 3 * 128 * ROW_BYTES, 8) == (3, 3)
     assert replay(64, 256, 160 * KIB, 8) == (4, 4)
+    assert replay(64, 32, 160 * KIB, 8, cap=8) == (8, 8)
