@@ -113,8 +113,8 @@ int moe_router_fused(const void* x, const float* router_w, const float* bias, in
                 "topk must be in 1..min(experts, 8)");
     MOE_REQUIRE(tokens <= INT_MAX / experts, MOE_ERR_CAPACITY, "tokens*experts exceeds int32");
     if (tokens == 0) return MOE_OK;
-    MOE_REQUIRE(x && router_w && bias && ids32 && weights, MOE_ERR_INVALID_ARGUMENT,
-                "null pointer");
+    // router_w == NULL: scratch already holds the split planes.
+    MOE_REQUIRE(x && bias && ids32 && weights, MOE_ERR_INVALID_ARGUMENT, "null pointer");
     const int64_t need = router_scratch_bytes(experts, hidden);
     MOE_REQUIRE(scratch && scratch_bytes >= need, MOE_ERR_WORKSPACE,
                 "router scratch needs %lld bytes, got %lld", (long long)need, (long long)scratch_bytes);

@@ -404,11 +404,13 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
                         uint16_t* planes, int64_t tokens, int hidden, int experts, int topk,
                         hipStream_t stream) {
     if (tokens == 0) return MOE_OK;
-    const int64_t n = static_cast<int64_t>(experts) * hidden;
-    hipLaunchKernelGGL(router_split_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0,
-                       stream, router_w, planes, n);
-    const int rc = check_launch("router_split_kernel");
-    if (rc != MOE_OK) return rc;
+    if (router_w != nullptr) {  // else planes already holds the split
+        const int64_t n = static_cast<int64_t>(experts) * hidden;
+        hipLaunchKernelGGL(router_split_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0,
+                           stream, router_w, planes, n);
+        const int rc = check_launch("router_split_kernel");
+        if (rc != MOE_OK) return rc;
+    }
     // Buffer offsets are 32-bit: 3*E*H*2 bytes of planes and 32 rows of x must fit.
     MOE_REQUIRE(hidden <= (1 << 20), MOE_ERR_UNSUPPORTED, "fused router supports hidden <= 1048576 (got %d)",
                 hidden);

@@ -82,19 +82,23 @@ class HipExtension:
 
         ``scratch`` (uint8, at least ``router_scratch_bytes(E, H)`` bytes, on the
         device) receives the bf16 split of the router weights; when omitted a
-        buffer is allocated for this call.
+        buffer is allocated for this call. ``router_weight=None`` reuses the
+        split ``scratch`` already holds from an earlier call with the same E, H.
         """
         _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,
                "expected BF16 GPU x[T,H]")
         tokens, hidden = x.shape
-        for name, t in (("router_weight", router_weight), ("bias", bias), ("ids32", ids32),
-                        ("weights", weights)):
+        for name, t in (("bias", bias), ("ids32", ids32), ("weights", weights)):
             _check_gpu_tensor(t, x, name)
         if ids64 is not None:
             _check_gpu_tensor(ids64, x, "ids64")
-        experts = router_weight.shape[0]
-        _check(router_weight.dtype == torch.float32 and router_weight.shape == (experts, hidden),
-               "expected FP32 router_weight[E,H]")
+        experts = bias.shape[0] if bias.dim() == 1 else -1
+        if router_weight is None:
+            _check(scratch is not None, "reusing the router split needs the scratch that holds it")
+        else:
+            _check_gpu_tensor(router_weight, x, "router_weight")
+            _check(router_weight.dtype == torch.float32 and router_weight.shape == (experts, hidden),
+                   "expected FP32 router_weight[E,H]")
         _check(bias.dtype == torch.float32 and bias.shape == (experts,), "expected FP32 bias[E]")
         topk = ids32.shape[1] if ids32.dim() == 2 else -1
         _check(ids32.shape == (tokens, topk) and ids32.dtype == torch.int32, "expected int32 ids[T,K]")

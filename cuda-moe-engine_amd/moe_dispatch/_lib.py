@@ -13,7 +13,7 @@ from functools import lru_cache
 from pathlib import Path
 
 LIBRARY_NAME = "libmoe_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1

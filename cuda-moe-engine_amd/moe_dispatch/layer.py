@@ -59,6 +59,10 @@ class MoEWeights:
     down: torch.Tensor
 
 
+def _capturing():
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 def make_weights(config, device, dtype, seed=42):
     """Seeded weights, drawn in the reference's order (``layer.py:38-59``).
 
@@ -127,6 +131,7 @@ class MoEBlock(torch.nn.Module):
         self._workspaces = {}
         self._route_buffers = {}
         self._router_scratch = None  # bf16 split of the router weights (fused router)
+        self._router_split_of = None  # (pointer, version, shape) of the weights the split holds
         self._extension = get_extension() if implementation != "torch" else None
 
     def set_routing_pattern(self, pattern):
@@ -157,15 +162,34 @@ class MoEBlock(torch.nn.Module):
             if self._router_scratch is None or self._router_scratch.device != x.device:
                 need = self._extension.router_scratch_bytes(self.config.experts, self.config.hidden)
                 self._router_scratch = torch.empty(need, dtype=torch.uint8, device=x.device)
+                self._router_split_of = None
+            # The split of the router weights is redone only when they may have
+            # changed (another tensor, or an in-place write, which bumps the
+            # version counter), and always inside a graph capture, so that every
+            # replay of the graph reads the weights as they are then.
+            split_of = self._router_split_key()
+            if split_of is not None and split_of == self._router_split_of and not _capturing():
+                router_weight = None
+            else:
+                router_weight = self.router_weight
             self._extension.router_fused_out(
-                x, self.router_weight, self.routing_bias, ids32, ids64, weights,
+                x, router_weight, self.routing_bias, ids32, ids64, weights,
                 scratch=self._router_scratch,
             )
+            self._router_split_of = split_of
             return ids32, ids64, weights
         logits = torch.nn.functional.linear(x.float(), self.router_weight) + self.routing_bias
         selected, ids64 = torch.topk(logits, self.config.topk, dim=-1)
         weights = torch.softmax(selected, dim=-1).contiguous()
         return ids64.to(torch.int32).contiguous(), ids64.contiguous(), weights
+
+    def _router_split_key(self):
+        w = self.router_weight
+        try:
+            version = w._version
+        except RuntimeError:  # inference tensors do not count versions
+            return None
+        return (w.data_ptr(), version, tuple(w.shape), w.device)
 
     def workspace(self, x):
         key = (x.shape[0], x.dtype, x.device)

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 3
+#define MOE_ABI_VERSION 4
 
 typedef enum {
     MOE_DTYPE_F32 = 0,
@@ -84,6 +84,9 @@ int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden);
  * router_w is split exactly into three bf16 planes (hi, mid, lo) in scratch
  * (moe_router_scratch_bytes bytes, 16-byte aligned) once per call; the
  * products x * part are exact and accumulate in fp32 on MFMA.
+ * router_w == NULL skips the split and uses the planes scratch already holds
+ * from an earlier call with the same E and H (for callers that know the
+ * router weights have not changed since; no reference counterpart).
  */
 int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
                      int64_t* ids64, float* weights, float* logits_out, void* scratch,

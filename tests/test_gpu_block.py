@@ -131,6 +131,26 @@ def test_block_is_deterministic():
     assert torch.equal(first, second)
 
 
+def test_router_weight_updates_are_seen():
+    """The fused router keeps the bf16 split of its weights between calls; an
+    in-place update or a new tensor must still route with the new weights."""
+    cfg = MoEConfig(256, 512, 16, 2)
+    block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=3)
+    twin = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=3)
+    x = torch.randn(300, 256, device="cuda").bfloat16()
+    block(x)
+    block(x)
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    for replace in (False, True):
+        new_w = torch.randn(16, 256, device="cuda", generator=gen) / 16
+        if replace:
+            block.router_weight = new_w.clone()
+        else:
+            block.router_weight.copy_(new_w)
+        twin.router_weight = new_w.clone()
+        assert torch.equal(block(x), twin(x))
+
+
 def test_empty_batch():
     block = MoEBlock(MoEConfig(64, 128, 8, 2), device="cuda", implementation="cuda_fused")
     out = block(torch.empty(0, 64, device="cuda", dtype=torch.bfloat16))

@@ -41,3 +41,23 @@ def test_graph_replays_match_eager(cfg, tokens):
     graph.replay()
     torch.cuda.synchronize()
     assert torch.equal(output, expected_other)
+
+
+def test_graph_replay_reads_router_weights_as_they_are():
+    """A captured forward re-splits the router weights on every replay, so an
+    in-place update after capture routes the replay with the new weights."""
+    cfg = MoEConfig(512, 1024, 8, 2)
+    block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=0)
+    twin = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=0)
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn(128, cfg.hidden, device="cuda", generator=gen).bfloat16()
+    block(x)  # the split is now held between calls
+    graph = capture_forward(block, x)
+    output = block.workspace(x).transport.output
+    new_w = torch.randn(cfg.experts, cfg.hidden, device="cuda", generator=gen) / cfg.hidden**0.5
+    block.router_weight.copy_(new_w)
+    twin.router_weight = new_w.clone()
+    expected = twin(x).clone()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(output, expected)

@@ -112,3 +112,29 @@ def test_fused_router_ties_go_to_lower_expert(ext, experts, topk):
     ids_ref, w_ref, _ = oracle.topk_route(np.zeros((tokens, experts), np.float32), to_np(bias), topk)
     np.testing.assert_array_equal(to_np(ids32), ids_ref)
     np.testing.assert_allclose(to_np(weights), w_ref, rtol=2e-6, atol=2e-6)
+
+
+def test_fused_router_reuses_a_held_split(ext):
+    """router_weight=None routes with the split the scratch already holds: the same
+    logits, ids and weights as passing the weights again, on new tokens."""
+    tokens, hidden, experts, topk = 300, 512, 16, 2
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    w = torch.randn(experts, hidden, device="cuda", generator=gen) / hidden**0.5
+    bias = torch.zeros(experts, device="cuda")
+    scratch = torch.empty(ext.router_scratch_bytes(experts, hidden), dtype=torch.uint8, device="cuda")
+    first = torch.randn(tokens, hidden, device="cuda", generator=gen).bfloat16()
+    x = torch.randn(tokens, hidden, device="cuda", generator=gen).bfloat16()
+
+    def route(tokens_in, weight):
+        out = (torch.empty(tokens, topk, device="cuda", dtype=torch.int32),
+               torch.empty(tokens, topk, device="cuda", dtype=torch.int64),
+               torch.empty(tokens, topk, device="cuda"),
+               torch.empty(tokens, experts, device="cuda"))
+        ext.router_fused_out(tokens_in, weight, bias, out[0], out[1], out[2], out[3], scratch=scratch)
+        return out
+
+    route(first, w)
+    reused = route(x, None)
+    fresh = route(x, w)
+    for a, b in zip(reused, fresh):
+        assert torch.equal(a, b)
