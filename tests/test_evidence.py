@@ -230,3 +230,21 @@ def test_verifier_does_not_need_torch():
             "from moe_dispatch import evidence; print(len(evidence.source_hashes()))" % str(package))
     proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=60)
     assert proc.returncode == 0, proc.stderr
+
+
+def test_committed_bundle_is_internally_consistent():
+    """profiles/evidence: the manifest holds, every statistic follows from its raw
+    samples and every validation passed. (Whether its source hashes match the
+    checkout is what ``verify`` adds; a later source change ends that match.)"""
+    from pathlib import Path
+
+    directory = Path(__file__).resolve().parents[1] / "profiles" / "evidence"
+    if not (directory / "manifest.json").exists():
+        pytest.skip("no committed evidence bundle")
+    assert set(evidence.check_manifest(directory)["sha256"]) == {"block_results.json", "results.json"}
+    block = json.loads((directory / "block_results.json").read_text())
+    summary = evidence.validate_block(block, hashes=block["source_hashes"])
+    assert summary["forward_comparisons_passed"] == 15 and summary["graph_replay_checks_passed"] == 15
+    assert summary["max_relative_l2_error"] < 5e-4
+    transport = evidence.summarize(evidence.read_results(directory / "results.json"))
+    assert transport["correctness_checks"] == 36 and transport["configurations"] == 12
