@@ -21,6 +21,7 @@ import math
 
 import torch
 
+from . import _lib
 from ._extension import get_extension
 from .experts import grouped_linear, resolve_backend, swiglu_reference
 from .reference import TorchWorkspace
@@ -132,6 +133,7 @@ class MoEBlock(torch.nn.Module):
         self._route_buffers = {}
         self._router_scratch = None  # bf16 split of the router weights (fused router)
         self._router_split_of = None  # (pointer, version, shape) of the weights the split holds
+        self._launches = {}  # cuda_fused: pre-validated launches per input signature
         self._extension = get_extension() if implementation != "torch" else None
 
     def set_routing_pattern(self, pattern):
@@ -241,12 +243,94 @@ class MoEBlock(torch.nn.Module):
             raise ValueError("input dtype/device must match expert weights")
         if x.shape[0] == 0:
             return torch.empty_like(x)
+        if self.implementation == "cuda_fused":
+            launches = self._launches.get((x.shape[0], x.device))
+            if launches is not None and launches.still_valid(self):
+                return launches(self, x)
         state = self.workspace(x)
         ids32, ids64, weights = self.route(x)
         state.transport.dispatch(x, ids32, ids64)
         output = self.experts_forward(state)
         state.transport.combine(output, weights)
+        if self.implementation == "cuda_fused":
+            # Every operator above validated its tensors; later calls of this
+            # shape reuse the checked arguments.
+            self._launches[(x.shape[0], x.device)] = _FusedLaunches(self, x, state)
         return state.transport.output
+
+
+class _FusedLaunches:
+    """The C-ABI calls of one validated cuda_fused forward, for reuse.
+
+    A forward through the validating operators (router_fused_out, dispatch,
+    the two grouped GEMMs, combine) fixes every argument but x's address and
+    the stream: workspace and weight pointers, sizes, the dtype code. Later
+    forwards of the same token count on the same device make the same five
+    calls with those arguments, as long as the weight and bias tensors are the
+    same objects at the same addresses (an in-place update keeps both, and the
+    router split follows the weights' version as in ``MoEBlock.route``). This
+    removes about 50 us of host work per forward (validation and stream
+    lookups), which dominates the eager latency of small batches.
+    """
+
+    def __init__(self, block, x, state):
+        cfg = block.config
+        t = state.transport
+        ids32, ids64, weights = block._route_buffers[(x.shape[0], x.device)]
+        self.lib = block._extension.lib
+        self.device_index = x.device.index if x.device.index is not None else torch.cuda.current_device()
+        self.tensors = (block.gate_up_weight, block.down_weight, block.routing_bias, block._router_scratch)
+        self.pointers = tuple(v.data_ptr() for v in self.tensors)
+        self.keep = (ids32, ids64, weights, t, state)  # the buffers below stay allocated
+        tokens, hidden = x.shape
+        rows = t.packed.shape[0]
+        scratch = block._router_scratch
+        self.router = (block.routing_bias.data_ptr(), ids32.data_ptr(), ids64.data_ptr(), weights.data_ptr(),
+                       None, scratch.data_ptr(), scratch.numel() * scratch.element_size(),
+                       tokens, hidden, cfg.experts, cfg.topk)
+        self.dispatch = (_lib.DTYPE_BF16, ids32.data_ptr(), t.counts.data_ptr(), t.offsets.data_ptr(), t.slots.data_ptr(),
+                         t.packed.data_ptr(), t.inverse.data_ptr(), t.scratch.data_ptr(),
+                         t.scratch.numel() * t.scratch.element_size(), tokens, hidden, cfg.experts, cfg.topk,
+                         t.alignment, rows, int(bool(t.vectorized)))
+        self.gateup = (t.packed.data_ptr(), block.gate_up_weight.data_ptr(), state.activated.data_ptr(),
+                       t.offsets.data_ptr(), rows, hidden, cfg.intermediate, cfg.experts)
+        self.down = (state.activated.data_ptr(), block.down_weight.data_ptr(), state.expert_output.data_ptr(),
+                     t.offsets.data_ptr(), rows, hidden, cfg.intermediate, cfg.experts)
+        self.combine = (state.expert_output.data_ptr(), _lib.DTYPE_BF16, t.inverse.data_ptr(), weights.data_ptr(),
+                        t.output.data_ptr(), tokens, hidden, cfg.topk, rows)
+        self.output = t.output
+        if x.dtype != torch.bfloat16:
+            raise RuntimeError("cuda_fused launches are bf16")
+
+    def still_valid(self, block):
+        tensors = (block.gate_up_weight, block.down_weight, block.routing_bias, block._router_scratch)
+        return all(a is b for a, b in zip(tensors, self.tensors)) and all(
+            v.data_ptr() == p for v, p in zip(tensors, self.pointers))
+
+    def __call__(self, block, x):
+        lib = self.lib
+        stream = _raw_stream(self.device_index)
+        x_ptr = x.data_ptr()
+        split_of = block._router_split_key()
+        if split_of is not None and split_of == block._router_split_of and not _capturing():
+            router_weight = None
+        else:
+            router_weight = block.router_weight.data_ptr()
+        lib.check(lib.moe_router_fused(x_ptr, router_weight, *self.router, stream), "router_fused_out")
+        block._router_split_of = split_of
+        lib.check(lib.moe_dispatch(x_ptr, *self.dispatch, stream), "dispatch")
+        lib.check(lib.moe_grouped_gateup_swiglu(*self.gateup, stream), "gateup_swiglu_out")
+        lib.check(lib.moe_grouped_gemm(*self.down, stream), "grouped_gemm_out")
+        lib.check(lib.moe_combine(*self.combine, stream), "combine_out")
+        return self.output
+
+
+def _raw_stream(device_index):
+    """The current stream's handle on a device (torch's own accessor when it has one)."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(device_index)
+    return torch.cuda.current_stream(device_index).cuda_stream
 
 
 @torch.inference_mode()

@@ -151,6 +151,59 @@ def test_router_weight_updates_are_seen():
         assert torch.equal(block(x), twin(x))
 
 
+@pytest.mark.parametrize("cfg,tokens,bias", [
+    (MoEConfig(512, 1024, 8, 2), 128, None),
+    (MoEConfig(256, 512, 16, 2), 777, "skewed"),
+    (MoEConfig(256, 128, 64, 6), 300, "zipf"),
+])
+def test_repeat_calls_match_validated_calls(cfg, tokens, bias):
+    """After its first (validated) forward a block reuses the checked launch
+    arguments; those forwards must equal a fresh block's validated forward."""
+    block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=5)
+    if bias == "skewed":
+        block.set_routing_pattern("skewed")
+    elif bias == "zipf":
+        block.set_routing_bias(torch.tensor(oracle.zipf_bias(cfg.experts, exponent=1.2, scale=1.75, seed=0)))
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    inputs = [torch.randn(tokens, cfg.hidden, device="cuda", generator=gen).bfloat16() for _ in range(3)]
+    first = block(inputs[0]).clone()
+    assert (tokens, inputs[0].device) in block._launches
+    assert torch.equal(block(inputs[0]), first)
+    for x in inputs[1:]:
+        fresh = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=5)
+        fresh.routing_bias.copy_(block.routing_bias)
+        assert torch.equal(block(x).clone(), fresh(x))
+
+
+def test_repeat_calls_follow_weight_changes_and_streams():
+    cfg = MoEConfig(256, 512, 8, 2)
+    block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=2)
+    twin = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=2)
+    x = torch.randn(200, 256, device="cuda").bfloat16()
+    block(x)
+    block(x)
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    # A new expert weight tensor (another address): the launches are rebuilt.
+    new_gate_up = (torch.randn(8, 1024, 256, device="cuda", generator=gen) / 16).bfloat16()
+    block.gate_up_weight = new_gate_up.clone()
+    twin.gate_up_weight = new_gate_up.clone()
+    assert torch.equal(block(x).clone(), twin(x))
+    # In-place updates of the down weights and the bias keep the addresses.
+    new_down = (torch.randn(8, 256, 512, device="cuda", generator=gen) / 22).bfloat16()
+    block.down_weight.copy_(new_down)
+    twin.down_weight.copy_(new_down)
+    block.set_routing_pattern("skewed")
+    twin.set_routing_pattern("skewed")
+    assert torch.equal(block(x).clone(), twin(x))
+    # Launches go to the current stream.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out = block(x).clone()
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(out, twin(x))
+
+
 def test_empty_batch():
     block = MoEBlock(MoEConfig(64, 128, 8, 2), device="cuda", implementation="cuda_fused")
     out = block(torch.empty(0, 64, device="cuda", dtype=torch.bfloat16))
