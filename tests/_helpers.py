@@ -96,7 +96,8 @@ def assert_near_bit_exact(got, ref, max_fraction=1e-4, max_steps=1.0):
     so on random data about 0.2-0.3% of single MFMA fp32 results differ from
     the model by one fp32 ulp. After rounding to
     bf16 that leaves about 1e-5 of the outputs one bf16 step away. Requires
-    at most ``max_fraction`` of the elements to differ, each by at most
+    at most ``max_fraction`` of the elements (but always allows one: a single
+    flip in a few thousand outputs is within that rate) to differ, each by at most
     ``max_steps`` bf16 steps of its value or 2^-10 of the tensor's RMS (a
     result near zero after cancellation sees the accumulator's ulp at the
     scale of its partial sums).
@@ -108,7 +109,8 @@ def assert_near_bit_exact(got, ref, max_fraction=1e-4, max_steps=1.0):
     if not differ.any():
         return
     fraction = differ.mean()
-    assert fraction <= max_fraction, f"{int(differ.sum())} of {got.size} elements differ ({fraction:.2e})"
+    assert int(differ.sum()) <= max(max_fraction * got.size, 1), (
+        f"{int(differ.sum())} of {got.size} elements differ ({fraction:.2e})")
     step = bf16_step(np.maximum(np.abs(got[differ]), np.abs(ref[differ])))
     rms = float(np.sqrt(np.mean(np.square(ref.astype(np.float64)))))
     bound = np.maximum(max_steps * step, 2.0**-10 * rms)

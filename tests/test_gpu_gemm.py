@@ -59,7 +59,8 @@ GEMM_CASES = [
 def test_grouped_gemm_matches_float64(ext, counts, alignment, n, k):
     experts = len(counts)
     a, offsets, rows = _inputs(counts, alignment, k, seed=n + k)
-    b = (torch.randn(experts, n, k, device="cuda") / k**0.5).bfloat16()
+    g = torch.Generator(device="cuda").manual_seed(3 * n + k)
+    b = (torch.randn(experts, n, k, device="cuda", generator=g) / k**0.5).bfloat16()
     c = torch.full((rows, n), 7.0, device="cuda").bfloat16()
     ext.grouped_gemm_out(a, b, offsets, c)
     exact = oracle.grouped_gemm(to_np(a), to_np(b), to_np(offsets), order="exact")
@@ -92,7 +93,8 @@ def test_schedule_does_not_change_results(ext, counts, alignment, n, k, swiglu, 
     """Every tile is written, and by the same MFMA chain, whatever the persistent grid."""
     experts = len(counts)
     a, offsets, rows = _inputs(counts, alignment, k, seed=n + 3 * k)
-    w = (torch.randn(experts, 2 * n if swiglu else n, k, device="cuda") / k**0.5).bfloat16()
+    g = torch.Generator(device="cuda").manual_seed(5 * n + k)
+    w = (torch.randn(experts, 2 * n if swiglu else n, k, device="cuda", generator=g) / k**0.5).bfloat16()
     run = ext.gateup_swiglu_out if swiglu else ext.grouped_gemm_out
 
     def once():
@@ -142,7 +144,8 @@ GATEUP_CASES = [
 def test_gateup_swiglu_matches_unfused_pipeline(ext, counts, alignment, hidden, inter):
     experts = len(counts)
     a, offsets, rows = _inputs(counts, alignment, hidden, seed=hidden + inter)
-    w = (torch.randn(experts, 2 * inter, hidden, device="cuda") / hidden**0.5).bfloat16()
+    g = torch.Generator(device="cuda").manual_seed(3 * hidden + inter)
+    w = (torch.randn(experts, 2 * inter, hidden, device="cuda", generator=g) / hidden**0.5).bfloat16()
     act = torch.full((rows, inter), 3.0, device="cuda").bfloat16()
     ext.gateup_swiglu_out(a, w, offsets, act)
     used = int(to_np(offsets)[-1])
