@@ -749,13 +749,14 @@ __device__ __forceinline__ RingPlan ring_plan(int n1, int n2, int grid, bool all
 
 struct RingSlot {
     int phase;  // 0 / 1 for phase 1 / 2; -1: no tile
-    int tile;   // index inside the phase
+    int tile;   // index inside the phase of the first tile
     int piece;  // -1, or 0 / 1 for the two 128-column halves
+    int count;  // tiles tile, tile + 1, ... of this slot (0 to 2)
 };
 
-// Tile `sub` (0 or 1) of virtual workgroup q.
-__device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int q, int sub) {
-    RingSlot s{-1, 0, -1};
+// The tiles of virtual workgroup q.
+__device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int q) {
+    RingSlot s{-1, 0, -1, 0};
     const int base = pl.rounds * grid;
     if (q < base) {
         // Column j of the XCD's slots, rotated by the round so that the
@@ -766,7 +767,7 @@ __device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int 
         const int cols = r < pl.full_rounds ? pl.cpr : (r == pl.full_rounds ? pl.last_cols : 0);
         if (j < cols) {
             const int tile = (pos % kNumXcd) * pl.per1 + r * pl.cpr + j;
-            if (sub == 0 && tile < pl.n1) s = RingSlot{0, tile, -1};
+            if (tile < pl.n1) s = RingSlot{0, tile, -1, 1};
             return s;
         }
         // A phase-2 slot: its index among the rounds' phase-2 slots, in q order.
@@ -778,10 +779,9 @@ __device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int 
         idx += (j - cols) * kNumXcd + pos % kNumXcd;
         const int lo = static_cast<int>(static_cast<int64_t>(idx) * pl.carried / pl.slots);
         const int hi = static_cast<int>(static_cast<int64_t>(idx + 1) * pl.carried / pl.slots);
-        if (lo + sub < hi) s = RingSlot{1, lo + sub, -1};
+        if (lo < hi) s = RingSlot{1, lo, -1, hi - lo};
         return s;
     }
-    if (sub != 0) return s;
     const int phase = pl.n2 > 0 ? 1 : 0;
     const int first = pl.n2 > 0 ? pl.carried : 0;
     const RingPhase& ph = pl.rest;
@@ -789,10 +789,10 @@ __device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int 
     if (v < ph.blocks) {
         const int per = ph.blocks / kNumXcd;
         const int tile = (v % kNumXcd) * per + v / kNumXcd;
-        if (tile < ph.main) s = RingSlot{phase, first + tile, -1};
+        if (tile < ph.main) s = RingSlot{phase, first + tile, -1, 1};
     } else if (v - ph.blocks < ph.pieces) {
         const int r = v - ph.blocks;
-        s = RingSlot{phase, first + ph.main + r / 2, r % 2};
+        s = RingSlot{phase, first + ph.main + r / 2, r % 2, 1};
     }
     return s;
 }
@@ -935,8 +935,9 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
     auto next = [&](int& q, int& sub) {
         RingWork w{false, 0, 0, 0, 0, 0};
         for (; q < plan.virtual_blocks; q += grid, sub = 0) {
-            for (; sub < 2; ++sub) {
-                w = ring_locate<SWIGLU>(p, table, ring_slot(plan, grid, q, sub));
+            const RingSlot s = ring_slot(plan, grid, q);
+            for (; sub < s.count; ++sub) {
+                w = ring_locate<SWIGLU>(p, table, RingSlot{s.phase, s.tile + sub, s.piece, 1});
                 if (w.valid) return w;
             }
         }
