@@ -1,8 +1,9 @@
 // Token transport kernels for gfx950: deterministic dispatch (per-chunk
 // histogram and stable ranks, then one pack kernel that rebuilds the expert
 // prefix from the small per-chunk table, writes destinations, copies rows and
-// zeroes padding) and the atomic-free weighted combine. Plus the standalone
-// SwiGLU kept for API parity.
+// zeroes padding; for at most 1024 assignments the pack kernel ranks them
+// itself) and the atomic-free weighted combine. Plus the standalone SwiGLU
+// kept for API parity.
 //
 // Reference behaviour: src/moe_dispatch/csrc/dispatch.cu:13-93 (count, scan,
 // pack, combine), :194-275 (aligned layout and padding), :277-323 (SwiGLU).
@@ -99,7 +100,14 @@ template <> __device__ __forceinline__ uint2 zero_vec<uint2>() { return make_uin
 template <> __device__ __forceinline__ uint32_t zero_vec<uint32_t>() { return 0u; }
 template <> __device__ __forceinline__ uint16_t zero_vec<uint16_t>() { return 0; }
 
-template <int VB>
+// COUNT (at most kSmallAssign assignments): no count_rank_kernel; every block
+// ranks all assignments itself (the same ballots, in flat order) and keeps
+// the expert totals and its own assignments' ranks, which saves a launch for
+// small batches. The ranks, and so every output, are the same as the
+// two-kernel path's.
+constexpr int kSmallAssign = 1024;
+
+template <int VB, bool COUNT>
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
     const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
@@ -113,6 +121,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     __shared__ int before[kMaxExperts];
     __shared__ int offs[kMaxExperts + 1];
     __shared__ int64_t dest[kPackMaxAssign];
+    __shared__ int own_rank[COUNT ? kPackMaxAssign : 1];
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
@@ -120,6 +129,50 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * pack_tokens;
     const int my_chunk = static_cast<int>(t0 / chunk_tokens);
 
+    if constexpr (COUNT) {
+        // (a') Every assignment in rounds of kPackThreads: totals in `total`, and
+        //      for this block's assignments the rank among earlier assignments
+        //      to the same expert (-1 for an out-of-range id).
+        const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+        const int64_t n_assign = tokens * topk;
+        const int64_t own_lo = t0 * topk;
+        const int64_t own_hi = min(t0 + pack_tokens, tokens) * topk;
+        if (tid < kMaxExperts) total[tid] = 0;
+        for (int64_t base = 0; base < n_assign; base += kPackThreads) {
+            for (int i = tid; i < (kPackThreads / kWave) * kMaxExperts; i += kPackThreads)
+                (&part_all[0][0])[i] = 0;
+            __syncthreads();
+            const int64_t p = base + tid;
+            const bool valid = p < n_assign;
+            const int e = valid ? ids[p] : -1;
+            const bool in_range = valid && e >= 0 && e < experts;
+            uint64_t same = __ballot(in_range);
+#pragma unroll
+            for (int b = 0; b < 6; ++b) {
+                const bool bit = (e >> b) & 1;
+                const uint64_t plane = __ballot(in_range && bit);
+                same &= bit ? plane : ~plane;
+            }
+            const int rank = __popcll(same & lanes_below);
+            if (in_range && rank == 0) part_all[wave][e] = __popcll(same);
+            __syncthreads();
+            if (valid && p >= own_lo && p < own_hi) {
+                int s = -1;
+                if (in_range) {
+                    s = total[e] + rank;
+                    for (int w = 0; w < wave; ++w) s += part_all[w][e];
+                }
+                own_rank[p - own_lo] = s;
+            }
+            __syncthreads();
+            if (tid < experts) {
+                int add = 0;
+                for (int w = 0; w < kPackThreads / kWave; ++w) add += part_all[w][tid];
+                total[tid] += add;
+            }
+            __syncthreads();
+        }
+    } else {
     // (a) Column sums of chunk_counts: all chunks, and chunks before mine.
     //     Thread tid always sees expert tid % experts_pow2 (a divisor of 256).
     {
@@ -142,12 +195,17 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
         }
     }
     __syncthreads();
+    }
     if (wave == 0) {
         int tot = 0, bef = 0;
         if (lane < experts) {
-            for (int w = 0; w < kPackThreads / kWave; ++w) {
-                tot += part_all[w][lane];
-                bef += part_before[w][lane];
+            if constexpr (COUNT) {
+                tot = total[lane];  // ranks are already global: nothing before
+            } else {
+                for (int w = 0; w < kPackThreads / kWave; ++w) {
+                    tot += part_all[w][lane];
+                    bef += part_before[w][lane];
+                }
             }
         }
         const int span = (tot + alignment - 1) / alignment * alignment;
@@ -178,13 +236,15 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
         const int e = ids[p];
         int64_t d = -1;
         if (e >= 0 && e < experts) {
-            const int r = slots[p];
+            const int r = COUNT ? own_rank[i] : slots[p];
             if (r >= 0) {
                 const int slot = before[e] + r;
                 d = static_cast<int64_t>(offs[e]) + slot;
                 slots[p] = slot;
                 inverse[p] = static_cast<int32_t>(d);
             }
+        } else if constexpr (COUNT) {
+            slots[p] = -1;  // (count_rank_kernel writes this on the other path)
         }
         dest[i] = d;
     }
@@ -362,7 +422,8 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
     const int64_t row_bytes = hidden * elem;
     const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes);
     const int64_t n_assign = tokens * topk;
-    if (plan.n_chunks > 0) {
+    const bool count_in_pack = n_assign <= kSmallAssign;
+    if (plan.n_chunks > 0 && !count_in_pack) {
         hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)),
                            dim3(kRankThreads), 0, stream, ids, slots, chunk_counts, n_assign,
                            experts, plan.chunk_tokens * topk);
@@ -377,12 +438,17 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
     }
     const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
     const dim3 grid(static_cast<unsigned>(plan.pack_blocks));
-#define MOE_PACK_CASE(VBV)                                                                   \
-    hipLaunchKernelGGL(pack_kernel<VBV>, grid, dim3(kPackThreads), 0, stream,                \
-                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets, \
-                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,  \
-                       alignment, plan.chunk_tokens, plan.pack_tokens,                        \
+#define MOE_PACK_LAUNCH(VBV, CNT)                                                              \
+    hipLaunchKernelGGL((pack_kernel<VBV, CNT>), grid, dim3(kPackThreads), 0, stream,            \
+                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets,   \
+                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,    \
+                       alignment, plan.chunk_tokens, plan.pack_tokens,                          \
                        static_cast<int>(plan.n_chunks), experts_pow2)
+#define MOE_PACK_CASE(VBV)                 \
+    if (count_in_pack)                     \
+        MOE_PACK_LAUNCH(VBV, true);        \
+    else                                   \
+        MOE_PACK_LAUNCH(VBV, false)
     switch (vb) {
         case 16: MOE_PACK_CASE(16); break;
         case 8: MOE_PACK_CASE(8); break;
@@ -391,6 +457,7 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
         default: return fail(MOE_ERR_UNSUPPORTED, "row size %lld bytes", (long long)row_bytes);
     }
 #undef MOE_PACK_CASE
+#undef MOE_PACK_LAUNCH
     return check_launch("pack_kernel");
 }
 

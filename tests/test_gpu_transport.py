@@ -73,11 +73,17 @@ def test_combine_k2_matches_torch_weighted_sum_exactly(ext):
     torch.testing.assert_close(ws.output, expected, rtol=0, atol=0)
 
 
-def test_out_of_range_ids_are_masked(ext):
-    x = torch.randn(6, 32, device="cuda").bfloat16()
-    ids = torch.tensor([[0, 9], [1, -1], [2, 2], [7, 0], [8, 3], [1, 1]], device="cuda", dtype=torch.int32)
-    ws = CudaWorkspace(6, 32, 8, 2, torch.bfloat16, alignment=1, extension=ext)
+@pytest.mark.parametrize("tokens", [6, 700])  # pack ranks the ids itself up to 1024 assignments
+def test_out_of_range_ids_are_masked(ext, tokens):
+    x = torch.randn(tokens, 32, device="cuda").bfloat16()
+    if tokens == 6:
+        ids = torch.tensor([[0, 9], [1, -1], [2, 2], [7, 0], [8, 3], [1, 1]], device="cuda", dtype=torch.int32)
+    else:
+        g = torch.Generator(device="cuda").manual_seed(13)
+        ids = torch.randint(-2, 11, (tokens, 2), device="cuda", generator=g, dtype=torch.int32)
+    ws = CudaWorkspace(tokens, 32, 8, 2, torch.bfloat16, alignment=1, extension=ext)
     ws.inverse.fill_(-7)
+    ws.slots.fill_(5)
     # Capacity T*K rows; invalid assignments are not counted and leave inverse untouched.
     ws.dispatch(x, ids)
     layout = oracle.dispatch_layout(to_np(ids), 8, 1)
