@@ -975,12 +975,13 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
     }
 }
 
-// Decode-sized launches (at most 128 packed rows in all): every expert has at
-// most one row tile, so the work is streaming the active experts' weights (at
-// T=1, 2 x 235 MB for the gate/up GEMM). The kernel is persistent like the
-// wide one: one workgroup per CU walks the tiles (active expert by active
-// expert, column tile fastest) and issues the next tile's first stages before
-// the current tile's epilogue. Tiles are narrow so that a single token's two
+// Weight-streaming launches (decode sizes, and small batches over many
+// experts; the launcher's rule is below): the work is streaming
+// the active experts' weights (at T=1, 2 x 235 MB for the gate/up GEMM). The
+// kernel is persistent like the wide one: workgroups walk the tiles (row
+// tiles of at most MAX_ROWS rows, expert by expert, column tile by column
+// tile) and issue the next tile's first stages before the current tile's
+// epilogue. Tiles are narrow so that a single token's two
 // experts still spread over the CUs: 64 activation columns (128 weight rows,
 // waves 2 x 2) for the gate/up GEMM, 64 output columns for the down GEMM, and
 // 32 (waves 4 x 1) when at most 64 rows are packed (at T=16 the 4 x 1 waves,
@@ -992,8 +993,9 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
 // KiB) so that two workgroups share a CU, which suits a token's 448 tiles
 // better than one workgroup per CU with a deeper ring (T=1: 93 vs 97 us).
 // Each output is the same MFMA chain in k order as on the wide path. MAX_ROWS
-// (64 or 128) bounds every expert's span; a span of at most 64 rows runs the
-// 64-row tile.
+// is 64 when the launch has at most 64 rows, else 128; a row tile of at most
+// 64 rows runs the 64-row instance. At C1 (T=128, E=8: about 32 rows per
+// expert) the wide tiles kept 64 (gate/up) and 16 (down) CUs busy.
 template <bool SWIGLU, int MAX_ROWS>
 constexpr int narrow_cols() { return SWIGLU || MAX_ROWS == 128 ? 64 : 32; }
 
@@ -1013,35 +1015,40 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmP
     static_assert(MAX_ROWS == 64 || MAX_ROWS == 128, "decode row tiles");
     __shared__ __attribute__((aligned(1024))) char lds[kLds];
     const int lane = threadIdx.x & 63;
+    // Lane e: expert e's first row, rows, row tiles of at most MAX_ROWS rows,
+    // and its first tile. Tiles go expert by expert, column tile by column
+    // tile, row tiles fastest (so an expert's row tiles share a weight slab).
     int off = 0, span = 0;
     if (lane < p.experts) {
         off = p.offsets[lane];
         span = max(p.offsets[lane + 1] - off, 0);
     }
-    const uint64_t active = __ballot(span > 0);
-    const int rank = __popcll(active & ((uint64_t{1} << lane) - 1));  // active experts before this lane's
-    const int tiles = __popcll(active) * p.n_tiles;
+    const int m_tiles = (span + MAX_ROWS - 1) / MAX_ROWS;
+    const int count = m_tiles * p.n_tiles;
+    const int incl = wave_inclusive_sum(count);
+    const int first = incl - count;
+    const int tiles = __builtin_amdgcn_readlane(incl, kWave - 1);
     const int k_steps = static_cast<int>(p.k / kStageK);
     struct Work {
         bool valid;
         int tall, expert, row0, row_end, col0;  // tall: more than 64 rows
     };
-    // Tile t: column tile t % n_tiles of the (t / n_tiles)-th active expert.
     auto locate = [&](int t) {
         Work w{false, 0, 0, 0, 0, 0};
         if (t >= tiles) return w;
-        const int k = t / p.n_tiles;
-        const uint64_t owner = __ballot(((active >> lane) & 1) != 0 && rank == k);
+        const uint64_t owner = __ballot(lane < p.experts && count > 0 && first <= t);
         if (owner == 0) return w;
-        const int e = __builtin_ctzll(owner);
-        const int row0 = __builtin_amdgcn_readlane(off, e);
-        const int rows = __builtin_amdgcn_readlane(span, e);  // <= p.rows <= MAX_ROWS (checked by the launcher)
-        w.row0 = row0;
-        w.row_end = static_cast<int>(min(static_cast<int64_t>(row0) + rows, p.rows));
+        const int e = 63 - __builtin_clzll(owner);
+        const int rel = t - __builtin_amdgcn_readlane(first, e);
+        const int me = __builtin_amdgcn_readlane(m_tiles, e);
+        const int n_tile = rel / me;
+        const int base = __builtin_amdgcn_readlane(off, e);
+        w.row0 = base + (rel - n_tile * me) * MAX_ROWS;
+        w.row_end = static_cast<int>(min(static_cast<int64_t>(base) + __builtin_amdgcn_readlane(span, e), p.rows));
         if (w.row0 < 0 || w.row0 >= w.row_end) return w;
         w.tall = MAX_ROWS == 128 && w.row_end - w.row0 > 64;
         w.expert = e;
-        w.col0 = (t - k * p.n_tiles) * COLS;
+        w.col0 = n_tile * COLS;
         w.valid = true;
         return w;
     };
@@ -1130,11 +1137,22 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     const int64_t m_bound = (rows + BM - 1) / BM + p.experts;
     int64_t blocks = m_bound * p.n_tiles;
     if (blocks == 0) return MOE_OK;
-    if (BM == 256 && BN == 256 && p.k % kStageK == 0 && rows <= 128) {
+    // Narrow tiles for weight streaming: at most 128 rows in all, or at most 128
+    // per expert on average when the wide tiles (rows spread evenly over the
+    // experts) would not give every CU one. Measured at C1 (E=8, ~32 rows each):
+    // gate/up 9.4 -> 7.2 us, down 11.6 -> 7.4 us; at C3 T=256 the gate/up GEMM's
+    // 256 wide tiles streamed faster than narrow ones (22.9 vs 24.9 us).
+    const int64_t per_expert = (rows + p.experts - 1) / p.experts;
+    const int64_t wide_tiles = static_cast<int64_t>(p.experts) * ((per_expert + BM - 1) / BM) * p.n_tiles;
+    const bool narrow = rows <= 128 || (rows <= 128 * static_cast<int64_t>(p.experts) &&
+                                        wide_tiles < device_cu_count());
+    if (BM == 256 && BN == 256 && p.k % kStageK == 0 && narrow) {
         GemmParams q = p;
-        const int cols = rows <= 64 ? narrow_cols<SWIGLU, 64>() : narrow_cols<SWIGLU, 128>();
+        const int max_rows = rows <= 64 ? 64 : 128;
+        const int cols = max_rows == 64 ? narrow_cols<SWIGLU, 64>() : narrow_cols<SWIGLU, 128>();
         q.n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
-        const int64_t tiles = static_cast<int64_t>(p.experts) * q.n_tiles;
+        // Upper bound on row tiles: sum_e ceil(span_e/max_rows) <= ceil(R/max_rows) + E.
+        const int64_t tiles = ((rows + max_rows - 1) / max_rows + p.experts) * q.n_tiles;
         if (tiles > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
         // As many workgroups as fit the CUs' LDS, at most one per tile.
         const uint32_t lds = rows <= 64 ? decode_lds_bytes<SWIGLU, 64>() : decode_lds_bytes<SWIGLU, 128>();
