@@ -274,7 +274,7 @@ def transport_bench(args):
     comb_bytes = oracle.combine_bytes(tokens, hidden, topk)
     d_gbs = disp_bytes / (d_us * 1e-6) / 1e9
     c_gbs = comb_bytes / (c_us * 1e-6) / 1e9
-    traffic = measured_traffic(args.config, ("count_rank_kernel", "pack_kernel<16>"))
+    traffic = measured_traffic(args.config, ("count_rank_kernel", "pack_kernel<16, false>"))
     result = {
         "metric": "MoE block fwd latency (us) + expert TFLOP/s % bf16 MFMA peak; dispatch GB/s",
         "value": round(mean_us, 2),

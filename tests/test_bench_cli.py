@@ -39,7 +39,7 @@ def test_measured_traffic_sums_kernels(tmp_path, monkeypatch):
 def test_committed_traffic_table_covers_the_bench_kernels():
     table = json.loads((ROOT / "profiles" / "hbm_traffic.json").read_text())
     assert "grouped_gemm_persistent_kernel<true>" in table["c4_t4096"]
-    assert {"count_rank_kernel", "pack_kernel<16>"} <= set(table["c2_transport"])
+    assert {"count_rank_kernel", "pack_kernel<16, false>"} <= set(table["c2_transport"])
 
 
 def test_gateup_roofline_picks_the_bound_by_intensity():
