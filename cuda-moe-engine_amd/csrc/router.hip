@@ -115,6 +115,13 @@ __global__ __launch_bounds__(256) void topk_route_kernel(const float* __restrict
 //  * router_ring_kernel (below) multiplies x by the planes and runs top-k.
 // ---------------------------------------------------------------------------
 
+constexpr int kRouterTokens = 16;
+constexpr int kRouterSplitTokens = 64;  // split-k routing up to this many tokens (E <= 16)
+constexpr int kRouterSplitSlices = 16;
+constexpr int kRouterSplitTiles = kRouterSplitTokens / kRouterTokens;
+constexpr int64_t kRouterPartialBytes =
+    static_cast<int64_t>(kRouterSplitTiles) * kRouterSplitSlices * kRouterTokens * 16 * 4;
+
 __global__ __launch_bounds__(256) void router_split_kernel(const float* __restrict__ w,
                                                            uint16_t* __restrict__ planes, int64_t n) {
     const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
@@ -164,9 +171,46 @@ __global__ __launch_bounds__(256) void router_split_kernel(const float* __restri
 // Rows of 128 bytes hold 8 chunks of 16 bytes; chunk c of row r sits at
 // physical chunk c ^ ((r >> 1) & 7), so 16 lanes reading 16 consecutive rows
 // at one chunk are conflict free.
+// Top-k over one token's biased logits held by eight lanes (lane `sub` holds
+// experts sub*EPL .. sub*EPL+EPL-1; -inf past E). K rounds of: argmax over
+// the lane's values (the lower expert wins a tie), the same across the eight
+// lanes with three xor shuffles, then the winner is removed -- the
+// reference's iterative argmax with ties to the lower id. Lane 0 writes.
+template <int EPL>
+__device__ __forceinline__ void select_eight_lanes(float (&v)[EPL], int sub, int topk, int64_t token,
+                                                   int32_t* ids32, int64_t* ids64, float* weights) {
+    float sel_v[kMaxTopk];
+    int sel_i[kMaxTopk];
+#pragma unroll
+    for (int k = 0; k < kMaxTopk; ++k) {
+        if (k < topk) {
+            float bv = v[0];
+            int bi = sub * EPL;
+#pragma unroll
+            for (int j = 1; j < EPL; ++j) {
+                const bool take = v[j] > bv;
+                bv = take ? v[j] : bv;
+                bi = take ? sub * EPL + j : bi;
+            }
+#pragma unroll
+            for (int msk = 1; msk < 8; msk <<= 1) {
+                const float ov = __shfl_xor(bv, msk);
+                const int oi = __shfl_xor(bi, msk);
+                const bool take = ov > bv || (ov == bv && oi < bi);
+                bv = take ? ov : bv;
+                bi = take ? oi : bi;
+            }
+            sel_v[k] = bv;
+            sel_i[k] = bi;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) v[j] = (sub * EPL + j == bi) ? -INFINITY : v[j];
+        }
+    }
+    if (sub == 0) write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
+}
+
 typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float rfloatx4_t __attribute__((ext_vector_type(4)));
-constexpr int kRouterTokens = 16;
 constexpr int kRouterRowBytes = 128;  // 64 k of one row
 constexpr uint32_t kRouterOob = 0x80000000u;  // a buffer offset past any router operand
 
@@ -196,12 +240,20 @@ struct RouterShape {
     static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-template <int NT, int MT>
+// SPLIT (at most kRouterSplitTokens tokens, E <= 16): block b takes token tile
+// b / slices and the k-slice b % slices of `per` stages, loads the whole slice
+// into its ring at once and writes the slice's partial logits to
+// partials[tile][slice][TB][EB]; router_reduce_kernel adds the slices in
+// slice order and selects. One token's routing at H=4096 otherwise streams its
+// 204 KB of weight planes through one CU, latency-bound (11 us). (A last-block
+// reduction inside this kernel needs a device-scope release per block, an L2
+// write-back that costs more than the second launch.)
+template <int NT, int MT, bool SPLIT = false>
 __global__ __launch_bounds__(256) void router_ring_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ planes,
     const float* __restrict__ bias, int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
     float* __restrict__ weights, float* __restrict__ logits_out, int64_t tokens, int hidden,
-    int experts, int topk) {
+    int experts, int topk, float* __restrict__ partials, int slices, int per) {
     using S = RouterShape<NT, MT>;
     constexpr int TB = S::TB, EB = S::EB, EBP = S::EBP, TPW = S::TPW, G = S::G, LPW = S::LPW;
     constexpr uint32_t A_STAGE = S::A_STAGE, B_STAGE = S::B_STAGE;
@@ -213,7 +265,9 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TB;
+    const int tile = SPLIT ? static_cast<int>(blockIdx.x) / slices : static_cast<int>(blockIdx.x);
+    const int slice = SPLIT ? static_cast<int>(blockIdx.x) - tile * slices : 0;
+    const int64_t t0 = static_cast<int64_t>(tile) * TB;
     const int64_t rows = min(static_cast<int64_t>(TB), tokens - t0);
     const int64_t row_bytes = static_cast<int64_t>(hidden) * 2;
     const __amdgpu_buffer_rsrc_t rsrc_x =
@@ -278,6 +332,33 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
 #pragma unroll
     for (int t = 0; t < TPW; ++t) acc[t] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
 
+    if constexpr (SPLIT) {
+        // The slice's stages (per <= STAGES, the launcher's condition) go to
+        // slots 0 .. n-1 at once; one wait, one barrier.
+        const int s_begin = slice * per;
+        const int n = min(per, k_stages - s_begin);
+        for (int s = 0; s < n; ++s) issue(s_begin + s, s);
+        wait_vm_lgkm<0>();
+        ring_barrier();
+        for (int s = 0; s < n; ++s) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if ((2 * s + h) % G != g) continue;
+                const char* abase = lds + va[h] + s * A_STAGE;
+                const char* bbase = lds + vb[h] + s * B_STAGE;
+                const rbf16x8_t a = *reinterpret_cast<const rbf16x8_t*>(abase);
+#pragma unroll
+                for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+                    for (int q = 2; q >= 0; --q) {
+                        const rbf16x8_t b = *reinterpret_cast<const rbf16x8_t*>(
+                            bbase + (q * EB + t * 16) * kRouterRowBytes);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[t], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    } else {
     // Stage s lives in slot s % STAGES; stages past the last are loaded as the
     // last one again (and not computed), so every iteration issues the same loads.
 #pragma unroll
@@ -317,7 +398,8 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
         group = group == 3 ? 0 : group + 1;
     }
     wait_vm_lgkm<0>();
-    if (threadIdx.x < experts) sbias[threadIdx.x] = bias[threadIdx.x];
+    }
+    if (!SPLIT && threadIdx.x < experts) sbias[threadIdx.x] = bias[threadIdx.x];
     // 16x16 result: lane l holds tokens 4*(l/16) + r of token tile mt, expert column l%16.
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
@@ -325,12 +407,18 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
         for (int r = 0; r < 4; ++r)
             part[(g * TB + mt * 16 + 4 * kq + r) * EBP + (nt0 + t) * 16 + m] = acc[t][r];
     __syncthreads();
+    if constexpr (SPLIT) {
+        // The slice's partial logits, its waves' partials added in wave order.
+        for (int i = threadIdx.x; i < TB * EB; i += 256) {
+            const int tl = i / EB, e = i % EB;
+            float logit = part[tl * EBP + e];
+#pragma unroll
+            for (int gg = 1; gg < G; ++gg) logit = logit + part[(gg * TB + tl) * EBP + e];
+            partials[((static_cast<int64_t>(tile) * slices + slice) * TB + tl) * EB + e] = logit;
+        }
+        return;
+    }
 
-    // Top-k: eight lanes per token (eight tokens per wave), each lane holding
-    // EB/8 consecutive experts. K rounds of: argmax over the lane's values
-    // (the lower expert wins a tie), the same across the eight lanes with
-    // three xor shuffles, then the winner is removed -- the reference's
-    // iterative argmax with ties to the lower id.
     constexpr int EPL = EB / 8;
     static_assert(EPL >= 1 && TB <= 32, "eight lanes per token, at most 32 tokens per block");
     const int tl = wave * 8 + (lane >> 3);
@@ -350,34 +438,45 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
                 v[j] = logit + sbias[e];
             }
         }
-        float sel_v[kMaxTopk];
-        int sel_i[kMaxTopk];
+        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights);
+    }
+}
+
+// Sum of a token tile's k-slices in slice order, the bias, and the same
+// selection as router_ring_kernel (16 tokens x 16 expert slots, E <= 16).
+__global__ __launch_bounds__(256) void router_reduce_kernel(
+    const float* __restrict__ partials, const float* __restrict__ bias, int32_t* __restrict__ ids32,
+    int64_t* __restrict__ ids64, float* __restrict__ weights, float* __restrict__ logits_out,
+    int64_t tokens, int experts, int topk, int slices) {
+    constexpr int TB = kRouterTokens, EB = 16, EPL = EB / 8;
+    static_assert(TB * EB == 256, "one thread per (token, expert)");
+    __shared__ float lg[TB][EB + 1];
+    const int tile = blockIdx.x;
+    {
+        const int tl = threadIdx.x / EB, e = threadIdx.x % EB;
+        const float* p = partials + (static_cast<int64_t>(tile) * slices * TB + tl) * EB + e;
+        float logit = p[0];
+        for (int s = 1; s < slices; ++s) logit = logit + p[static_cast<int64_t>(s) * TB * EB];
+        lg[tl][e] = logit;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int tl = (threadIdx.x >> 6) * 8 + (lane >> 3);
+    const int sub = lane & 7;
+    const int64_t token = static_cast<int64_t>(tile) * TB + tl;
+    if (tl < TB && token < tokens) {  // 32 lane groups, 16 tokens; uniform across each group of eight lanes
+        float v[EPL];
 #pragma unroll
-        for (int k = 0; k < kMaxTopk; ++k) {
-            if (k < topk) {
-                float bv = v[0];
-                int bi = sub * EPL;
-#pragma unroll
-                for (int j = 1; j < EPL; ++j) {
-                    const bool take = v[j] > bv;
-                    bv = take ? v[j] : bv;
-                    bi = take ? sub * EPL + j : bi;
-                }
-#pragma unroll
-                for (int msk = 1; msk < 8; msk <<= 1) {
-                    const float ov = __shfl_xor(bv, msk);
-                    const int oi = __shfl_xor(bi, msk);
-                    const bool take = ov > bv || (ov == bv && oi < bi);
-                    bv = take ? ov : bv;
-                    bi = take ? oi : bi;
-                }
-                sel_v[k] = bv;
-                sel_i[k] = bi;
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) v[j] = (sub * EPL + j == bi) ? -INFINITY : v[j];
+        for (int j = 0; j < EPL; ++j) {
+            const int e = sub * EPL + j;
+            v[j] = -INFINITY;
+            if (e < experts) {
+                const float logit = lg[tl][e];
+                if (logits_out) logits_out[token * experts + e] = logit;
+                v[j] = logit + bias[e];
             }
         }
-        if (sub == 0) write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
+        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights);
     }
 }
 
@@ -416,7 +515,15 @@ int launch_topk_route(const float* logits, const float* bias, int32_t* ids32, in
     return check_launch("topk_route_kernel");
 }
 
-int64_t router_scratch_bytes(int64_t experts, int64_t hidden) { return 3 * experts * hidden * 2; }
+// The three bf16 planes, then (256-byte aligned) the split path's partial
+// logits [tiles][slices][16 tokens][16 experts] fp32.
+static int64_t router_partials_offset(int64_t experts, int64_t hidden) {
+    return (3 * experts * hidden * 2 + 255) & ~static_cast<int64_t>(255);
+}
+
+int64_t router_scratch_bytes(int64_t experts, int64_t hidden) {
+    return router_partials_offset(experts, hidden) + kRouterPartialBytes;
+}
 
 int launch_router_fused(const uint16_t* x, const float* router_w, const float* bias,
                         int32_t* ids32, int64_t* ids64, float* weights, float* logits_out,
@@ -433,11 +540,32 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
     // Buffer offsets are 32-bit: 3*E*H*2 bytes of planes and 32 rows of x must fit.
     MOE_REQUIRE(hidden <= (1 << 20), MOE_ERR_UNSUPPORTED, "fused router supports hidden <= 1048576 (got %d)",
                 hidden);
+    const int k_stages = (hidden + 63) / 64;
+    constexpr int kSplitMaxPer = RouterShape<1, 1>::STAGES;  // a slice fits the ring at once
+    if (experts <= 16 && tokens <= kRouterSplitTokens && k_stages >= 16 &&
+        k_stages <= kRouterSplitSlices * kSplitMaxPer) {
+        // Split k: slices of about 8 stages (64 KiB of loads per workgroup),
+        // none empty.
+        const int per = (k_stages + min(kRouterSplitSlices, (k_stages + 7) / 8) - 1) /
+                        min(kRouterSplitSlices, (k_stages + 7) / 8);
+        const int slices = (k_stages + per - 1) / per;
+        const int tiles = static_cast<int>((tokens + kRouterTokens - 1) / kRouterTokens);
+        float* partials = reinterpret_cast<float*>(reinterpret_cast<char*>(planes) +
+                                                   router_partials_offset(experts, hidden));
+        hipLaunchKernelGGL((router_ring_kernel<1, 1, true>), dim3(static_cast<unsigned>(tiles * slices)),
+                           dim3(256), 0, stream, x, planes, bias, ids32, ids64, weights, logits_out, tokens,
+                           hidden, experts, topk, partials, slices, per);
+        const int rs = check_launch("router_ring_kernel");
+        if (rs != MOE_OK) return rs;
+        hipLaunchKernelGGL(router_reduce_kernel, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream,
+                           partials, bias, ids32, ids64, weights, logits_out, tokens, experts, topk, slices);
+        return check_launch("router_reduce_kernel");
+    }
 #define MOE_ROUTER_CASE(NTV, MTV)                                                                      \
     hipLaunchKernelGGL((router_ring_kernel<NTV, MTV>),                                                 \
                        dim3(static_cast<unsigned>((tokens + kRouterTokens * MTV - 1) / (kRouterTokens * MTV))), \
                        dim3(256), 0, stream, x, planes, bias, ids32, ids64, weights, logits_out, tokens, \
-                       hidden, experts, topk)
+                       hidden, experts, topk, nullptr, 1, 0)
     // Token tiles per block: one for E <= 16 (the four waves split k), two
     // above (the waves split the 16x16 output tiles).
     if (experts <= 16) {

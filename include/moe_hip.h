@@ -73,7 +73,9 @@ const char* moe_last_error(void);
 int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64_t* ids64,
                    float* weights, int64_t tokens, int64_t experts, int64_t topk, void* stream);
 
-/* Bytes of scratch moe_router_fused needs for (E, H): the bf16 split of router_w. */
+/* Bytes of scratch moe_router_fused needs for (E, H): the bf16 split of
+ * router_w, then 64 KiB of partial logits for the small-batch (T <= 64,
+ * E <= 16) split-k path. */
 int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden);
 
 /*
@@ -87,6 +89,7 @@ int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden);
  * router_w == NULL skips the split and uses the planes scratch already holds
  * from an earlier call with the same E and H (for callers that know the
  * router weights have not changed since; no reference counterpart).
+ * Calls that share one scratch must not overlap in time.
  */
 int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
                      int64_t* ids64, float* weights, float* logits_out, void* scratch,

@@ -64,9 +64,14 @@ def test_validation_errors_without_launching():
     assert lib.moe_grouped_gemm(1, 1, 1, 0, 0, 1 << 15, 1 << 15, 8, None) == 0  # 2 GiB: accepted (no rows)
     # hidden 12 is not a multiple of 8; then a scratch buffer below the split's size.
     assert lib.moe_router_fused(1, 1, 1, 1, 1, 1, None, 16, 1 << 20, 4, 12, 8, 2, None) == 2
-    assert lib.moe_router_scratch_bytes(8, 64) == 3 * 8 * 64 * 2
+    # Three bf16 planes (rounded up to 256 bytes), then the small-batch split's
+    # fp32 partial logits: 4 token tiles x 16 slices x 16 tokens x 16 experts.
+    partials = 4 * 16 * 16 * 16 * 4
+    assert lib.moe_router_scratch_bytes(8, 64) == 3 * 8 * 64 * 2 + partials
+    assert lib.moe_router_scratch_bytes(5, 72) == 2304 + partials  # 2160 rounded up
     assert lib.moe_router_scratch_bytes(65, 64) == -1
-    assert lib.moe_router_fused(16, 16, 16, 16, 16, 16, None, 16, 3 * 8 * 64 * 2 - 1, 4, 64, 8, 2, None) == 4
+    need = lib.moe_router_scratch_bytes(8, 64)
+    assert lib.moe_router_fused(16, 16, 16, 16, 16, 16, None, 16, need - 1, 4, 64, 8, 2, None) == 4
     assert b"router scratch needs" in lib.moe_last_error()
     # The persistent GEMM's workgroup bound (scheduling only; no launch here).
     assert lib.moe_set_gemm_workgroups(-1) == 1

@@ -67,7 +67,11 @@ def test_zero_logits_known_answer_and_empty_batch(ext):
 @pytest.mark.parametrize(
     "tokens,hidden,experts,topk",
     [(1, 512, 8, 2), (33, 512, 8, 1), (257, 1024, 16, 2), (300, 2048, 64, 6), (64, 4096, 8, 2),
-     (100, 136, 5, 3), (1000, 72, 32, 4), (8192, 2048, 64, 6)],
+     (100, 136, 5, 3), (1000, 72, 32, 4), (8192, 2048, 64, 6),
+     # Split-k routing (tokens <= 64, E <= 16, 16..256 stages of 64 hidden):
+     # one token; a ragged last stage inside the last slice; the largest split
+     # (16 slices of 16 stages); one stage past it (the single-workgroup path).
+     (1, 4096, 8, 2), (16, 4096, 16, 6), (33, 2040, 12, 3), (50, 16384, 4, 2), (3, 16448, 8, 2)],
 )
 def test_fused_router_matches_oracle(ext, tokens, hidden, experts, topk):
     generator = torch.Generator(device="cuda").manual_seed(tokens + hidden)
@@ -95,12 +99,13 @@ def test_fused_router_matches_oracle(ext, tokens, hidden, experts, topk):
     np.testing.assert_array_equal(np.sort(to_np(ids32)[safe], 1), np.sort(ids_ref[safe], 1))
 
 
+@pytest.mark.parametrize("tokens,hidden", [(70, 128), (40, 2048)])
 @pytest.mark.parametrize("experts,topk", [(8, 2), (16, 5), (32, 4), (64, 6), (64, 8)])
-def test_fused_router_ties_go_to_lower_expert(ext, experts, topk):
+def test_fused_router_ties_go_to_lower_expert(ext, experts, topk, tokens, hidden):
     """Zero activations make every logit exactly 0, so the selection is decided by a
     bias full of repeated values: the fused top-k must keep the lower expert id on
-    every tie, like the reference (``csrc/dispatch.cu:331-333``)."""
-    tokens, hidden = 70, 128
+    every tie, like the reference (``csrc/dispatch.cu:331-333``). 40 x 2048 with
+    E <= 16 takes the split-k path and its separate selection kernel."""
     x = torch.zeros(tokens, hidden, device="cuda", dtype=torch.bfloat16)
     w = torch.randn(experts, hidden, device="cuda") / hidden**0.5
     levels = torch.tensor([0.0, 1.0, 2.0, 0.5], device="cuda")
@@ -114,10 +119,12 @@ def test_fused_router_ties_go_to_lower_expert(ext, experts, topk):
     np.testing.assert_allclose(to_np(weights), w_ref, rtol=2e-6, atol=2e-6)
 
 
-def test_fused_router_reuses_a_held_split(ext):
+@pytest.mark.parametrize("tokens,hidden", [(300, 512), (8, 4096)])
+def test_fused_router_reuses_a_held_split(ext, tokens, hidden):
     """router_weight=None routes with the split the scratch already holds: the same
-    logits, ids and weights as passing the weights again, on new tokens."""
-    tokens, hidden, experts, topk = 300, 512, 16, 2
+    logits, ids and weights as passing the weights again, on new tokens (8 x 4096:
+    the split-k path, whose partial logits follow the planes in the scratch)."""
+    experts, topk = 16, 2
     gen = torch.Generator(device="cuda").manual_seed(5)
     w = torch.randn(experts, hidden, device="cuda", generator=gen) / hidden**0.5
     bias = torch.zeros(experts, device="cuda")
