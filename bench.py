@@ -188,7 +188,7 @@ def measured_traffic(config, kernels):
     return total
 
 
-def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, launch_us):
+def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, launch_us, cus=None):
     """Roofline entry for the gate/up GEMM + SwiGLU launch.
 
     Algorithmic bytes per launch: the weights of the experts that hold rows
@@ -196,11 +196,25 @@ def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, 
     activated output written once (assignments x I bf16). When flop/byte is below
     the MI355X ridge point (2500 TFLOP/s / 8 TB/s = 312.5) the launch is bound by
     HBM and the entry is in GB/s; otherwise by the bf16 MFMA peak, in TFLOP/s.
-    Launches of at most 128 packed rows run the 64-column decode kernel.
+    The kernel is the one the launcher picks (``launch_gemm_t`` in
+    ``csrc/gemm.hip``): the weight-streaming (decode) kernel when the buffer
+    has at most 128 rows, or at most 128 per expert while the 256 x 256 tiles
+    (rows spread evenly over the experts) would number fewer than the CUs
+    (``cus``; default: the current GPU's, 256 without one).
     """
+    import torch
+
+    def ceil_div(a, b):
+        return -(-a // b)
+
+    experts = len(counts)
     active = int((counts > 0).sum())
     byte = 2.0 * (active * 2 * inter * hidden + n_assign * hidden + n_assign * inter)
-    kernel = "grouped_gemm_decode_kernel<true>" if packed_rows <= 128 else "grouped_gemm_persistent_kernel<true>"
+    if cus is None:
+        cus = torch.cuda.get_device_properties(0).multi_processor_count if torch.cuda.is_available() else 256
+    wide_tiles = experts * ceil_div(ceil_div(packed_rows, experts), 256) * ceil_div(inter, 128)
+    decode = hidden % 64 == 0 and (packed_rows <= 128 or (packed_rows <= 128 * experts and wide_tiles < cus))
+    kernel = "grouped_gemm_decode_kernel<true>" if decode else "grouped_gemm_persistent_kernel<true>"
     entry = {"kernel": kernel + " (gate/up GEMM + SwiGLU epilogue)"}
     if flop / byte < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
         achieved = byte / (launch_us * 1e-6) / 1e9

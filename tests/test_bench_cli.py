@@ -59,3 +59,8 @@ def test_gateup_roofline_picks_the_bound_by_intensity():
     assert pre["kernel"].startswith("grouped_gemm_persistent_kernel<true>")
     assert abs(pre["achieved"] - 4.0 * 8192 * h * i / 1e-3 / 1e12) < 0.1
     assert list(pre)[0] == "bound"
+    # 320 rows over 8 experts (T=128, H=512, I=1024): 64 wide tiles for 256 CUs, so
+    # the launcher takes the weight-streaming kernel; with 32 CUs the wide one.
+    c1 = (np.array([32] * 8), 320, 512, 1024, 256, 4.0 * 256 * 512 * 1024, 10.0)
+    assert bench.gateup_roofline("none", *c1, cus=256)["kernel"].startswith("grouped_gemm_decode_kernel<true>")
+    assert bench.gateup_roofline("none", *c1, cus=32)["kernel"].startswith("grouped_gemm_persistent_kernel<true>")
