@@ -334,9 +334,7 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // row0 + SMT*64) of one expert (clamped to row_end) by BNT weight rows from
 // output column col0, in the first LDS_BYTES of `lds`, at most MAXS stages
 // deep. The four waves split the tile as (4/WC) row blocks x WC column blocks.
-// KROT: the tile's k chain starts at stage krot and wraps round (stage i of the
-// ring holds k-step (krot + i) mod k_steps), for the weight-streaming kernel.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2, int MAXS = 4, bool KROT = false>
+template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2, int MAXS = 4>
 struct RingOps {
     static constexpr int WAVES = kRingThreads / kWave;
     static constexpr int TM = SMT * 64;
@@ -369,11 +367,10 @@ struct RingOps {
     uint32_t a_off[A_LOADS], b_off[B_LOADS];
     char* lds;
     int wave;
-    int krot, ksteps;  // used when KROT
 
     __device__ __forceinline__ RingOps(const GemmParams& p, char* lds_, int expert, int64_t col0,
-                                       int64_t row0, int64_t row_end, int krot_ = 0)
-        : lds(lds_), krot(krot_), ksteps(static_cast<int>(p.k / kStageK)) {
+                                       int64_t row0, int64_t row_end)
+        : lds(lds_) {
         const int lane = threadIdx.x & 63;
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int64_t K = p.k;
@@ -406,20 +403,11 @@ struct RingOps {
     }
     }
     // Load l of stage kt into ring slot st, of A and of B.
-    __device__ __forceinline__ int kstep(int kt) const {
-        if constexpr (KROT) {
-            kt += krot;
-            kt -= kt >= ksteps ? ksteps : 0;
-        }
-        return kt;
-    }
     __device__ __forceinline__ void issue_a(int kt, int st, int l) const {
-        kt = kstep(kt);
         dma16(rsrc_a, lds + st * A_STAGE + (wave * A_LOADS + l) * 1024, a_off[l],
               static_cast<uint32_t>(kt) * kRowBytes);
     }
     __device__ __forceinline__ void issue_b(int kt, int st, int l) const {
-        kt = kstep(kt);
         dma16(rsrc_b, lds + B_BASE + st * B_STAGE + (wave * B_LOADS + l) * 1024, b_off[l],
               static_cast<uint32_t>(kt) * kRowBytes);
     }
@@ -460,12 +448,11 @@ struct NoHook {
 // before the first read instead of counting loads. hook: runs once the
 // k-loop is done and every wave has finished with the ring (it may refill
 // LDS), before the epilogue.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4,
-          bool KROT = false>
+template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end, bool own_prologue = true,
-                                          bool wait_all = false, const Hook& hook = Hook{}, int krot = 0) {
-    using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC, MAXS, KROT>;
+                                          bool wait_all = false, const Hook& hook = Hook{}) {
+    using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC, MAXS>;
     constexpr int WTM = R::WTM, WTN = R::WTN, FA = R::FA, FB = R::FB;
     constexpr int A_LOADS = R::A_LOADS, B_LOADS = R::B_LOADS;
     constexpr int SA = R::SA, SB = R::SB;
@@ -476,7 +463,7 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     const int wm = wave / WC;
     const int wn = wave % WC;
     const int64_t K = p.k;
-    const R ops(p, lds, expert, col0, row0, row_end, krot);
+    const R ops(p, lds, expert, col0, row0, row_end);
     auto issue_a = [&](int kt, int st, int l) { ops.issue_a(kt, st, l); };
     auto issue_b = [&](int kt, int st, int l) { ops.issue_b(kt, st, l); };
 
@@ -1005,37 +992,21 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
 // The 64-row gate/up instance is the exception: it keeps three stages (72
 // KiB) so that two workgroups share a CU, which suits a token's 448 tiles
 // better than one workgroup per CU with a deeper ring (T=1: 93 vs 97 us).
-// When the weight rows are a power of two apart (k_steps a power of two),
-// every workgroup reading k-step s of its rows at the same time lands on a
-// few memory channels: a read probe of 256-row blocks 8 KiB apart streams at
-// 4.4 TB/s in lockstep and 5.3 TB/s with the blocks' starting k-steps spread.
-// Such launches (ROT) therefore start each tile's k chain at a column- and
-// expert-dependent k-step and wrap round (H=4096, I=14336 gate/up GEMM: T=1
-// 90 -> 84 us, T=16 337 -> 314 us); each output's MFMA chain then runs over
-// the k-steps in that rotated order. Otherwise each output is the same MFMA
-// chain in k order as on the wide path.
-// MAX_ROWS is 64 when the launch has at most 64 rows, else 128; a row tile of
-// at most 64 rows runs the 64-row instance. At C1 (T=128, E=8: about 32 rows per
+// Each output is the same MFMA chain in k order as on the wide path. MAX_ROWS
+// is 64 when the launch has at most 64 rows, else 128; a row tile of at most
+// 64 rows runs the 64-row instance. At C1 (T=128, E=8: about 32 rows per
 // expert) the wide tiles kept 64 (gate/up) and 16 (down) CUs busy.
 template <bool SWIGLU, int MAX_ROWS>
 constexpr int narrow_cols() { return SWIGLU || MAX_ROWS == 128 ? 64 : 32; }
 
 constexpr int kDecodeStages = 8;
-// k-chain rotation of a weight-streaming tile (the ROT instances): first
-// k-step (kRotColBlock * (col / 64) + kRotExpert * expert) mod k_steps. Odd
-// multipliers spread consecutive column blocks over all k-steps. Used when
-// k_steps is a power of two of at least kRotMinSteps: at k = 512 and 1024
-// (8 and 16 steps, 8 MiB of weights per GEMM) rotation gained nothing.
-constexpr int kRotColBlock = 7;
-constexpr int kRotExpert = 37;
-constexpr int kRotMinSteps = 32;
 
 template <bool SWIGLU, int MAX_ROWS>
 constexpr uint32_t decode_lds_bytes() {
     return SWIGLU && MAX_ROWS == 64 ? 3 * (64 + 2 * narrow_cols<SWIGLU, MAX_ROWS>()) * kRowBytes : kRingBytes;
 }
 
-template <bool SWIGLU, int MAX_ROWS, bool ROT>
+template <bool SWIGLU, int MAX_ROWS>
 __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmParams p) {
     constexpr int COLS = narrow_cols<SWIGLU, MAX_ROWS>();
     constexpr int BNT = SWIGLU ? 2 * COLS : COLS;
@@ -1061,10 +1032,9 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmP
     struct Work {
         bool valid;
         int tall, expert, row0, row_end, col0;  // tall: more than 64 rows
-        int krot;                               // first k-step of the chain
     };
     auto locate = [&](int t) {
-        Work w{false, 0, 0, 0, 0, 0, 0};
+        Work w{false, 0, 0, 0, 0, 0};
         if (t >= tiles) return w;
         const uint64_t owner = __ballot(lane < p.experts && count > 0 && first <= t);
         if (owner == 0) return w;
@@ -1079,34 +1049,31 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmP
         w.tall = MAX_ROWS == 128 && w.row_end - w.row0 > 64;
         w.expert = e;
         w.col0 = n_tile * COLS;
-        w.krot = ROT ? (kRotColBlock * (w.col0 / 64) + kRotExpert * e) & (k_steps - 1) : 0;
         w.valid = true;
         return w;
     };
     auto prologue = [&](const Work& w) {
         if constexpr (MAX_ROWS == 128) {
             if (w.tall) {
-                RingOps<2, BNT, SWIGLU, kLds, WC, kDecodeStages, ROT>(p, lds, w.expert, w.col0, w.row0,
-                                                                       w.row_end, w.krot)
+                RingOps<2, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
                     .prologue(k_steps);
                 return;
             }
         }
-        RingOps<1, BNT, SWIGLU, kLds, WC, kDecodeStages, ROT>(p, lds, w.expert, w.col0, w.row0, w.row_end,
-                                                               w.krot)
+        RingOps<1, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
             .prologue(k_steps);
     };
     auto run = [&](const Work& w, bool wait_all, const auto& hook) {
         using Hook = std::decay_t<decltype(hook)>;
         if constexpr (MAX_ROWS == 128) {
             if (w.tall) {
-                ring_tile<2, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages, ROT>(
-                    p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook, w.krot);
+                ring_tile<2, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0,
+                                                                                w.row_end, false, wait_all, hook);
                 return;
             }
         }
-        ring_tile<1, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages, ROT>(p, lds, w.expert, w.col0, w.row0,
-                                                                       w.row_end, false, wait_all, hook, w.krot);
+        ring_tile<1, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end,
+                                                                        false, wait_all, hook);
     };
     int t = blockIdx.x;
     Work cur = locate(t);
@@ -1123,10 +1090,6 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmP
             // are uniform; they go back to scalar registers after the asm.)
             Work w = nxt;
             asm volatile("" : "+v"(w.tall), "+v"(w.expert), "+v"(w.row0), "+v"(w.row_end), "+v"(w.col0));
-            if constexpr (ROT) {
-                asm volatile("" : "+v"(w.krot));
-                w.krot = __builtin_amdgcn_readfirstlane(w.krot);
-            }
             w.tall = __builtin_amdgcn_readfirstlane(w.tall);
             w.expert = __builtin_amdgcn_readfirstlane(w.expert);
             w.row0 = __builtin_amdgcn_readfirstlane(w.row0);
@@ -1195,17 +1158,12 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
         const uint32_t lds = rows <= 64 ? decode_lds_bytes<SWIGLU, 64>() : decode_lds_bytes<SWIGLU, 128>();
         int64_t grid = static_cast<int64_t>(device_cu_count()) * (kRingBytes / lds);
         if (tiles < grid) grid = tiles;
-        const int64_t k_steps = p.k / kStageK;
-        const bool rot = k_steps >= kRotMinSteps && (k_steps & (k_steps - 1)) == 0;
-#define MOE_DECODE_LAUNCH(ROWS, ROTV)                                                                   \
-    hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, ROWS, ROTV>), dim3(static_cast<unsigned>(grid)), \
-                       dim3(kRingThreads), 0, stream, q)
-        if (rows <= 64) {
-            if (rot) MOE_DECODE_LAUNCH(64, true); else MOE_DECODE_LAUNCH(64, false);
-        } else {
-            if (rot) MOE_DECODE_LAUNCH(128, true); else MOE_DECODE_LAUNCH(128, false);
-        }
-#undef MOE_DECODE_LAUNCH
+        if (rows <= 64)
+            hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 64>), dim3(static_cast<unsigned>(grid)),
+                               dim3(kRingThreads), 0, stream, q);
+        else
+            hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 128>), dim3(static_cast<unsigned>(grid)),
+                               dim3(kRingThreads), 0, stream, q);
         return check_launch("grouped_gemm_decode_kernel");
     }
     if (BM == 256 && BN == 256 && p.k % kStageK == 0) {

@@ -41,13 +41,7 @@ Pinning (what checks each function; see tests/test_oracle.py)
   and the "mfma" order within the fp32 error bound of it); the "mfma" order
   against a pure-Python loop over k-groups on tiny inputs; on the GPU the
   kernels match the "mfma" order in >99.99% of bf16 outputs (the rest one
-  bf16 step away). ``k_rotation``: a zero table is the ascending order; with
-  integer-valued operands every order is exact, so a rotation that moved a's
-  k against b's would show; a pure-Python loop over the rotated k-groups on
-  tiny inputs; on the GPU, the weight-streaming launches match the rotated
-  order as closely as the others match the ascending one.
-* ``decode_k_rotation``: the closed form on a few columns and experts, and
-  None for k/64 below 32 or not a power of two.
+  bf16 step away).
 * ``block_forward``: the restated ``token_major_oracle`` (dense, token-major,
   independent of the permutation).
 """
@@ -71,7 +65,6 @@ __all__ = [
     "combine",
     "swiglu",
     "grouped_gemm",
-    "decode_k_rotation",
     "exp_f32",
     "silu_f32",
     "block_forward",
@@ -273,8 +266,7 @@ def pack(x: np.ndarray, layout: dict, topk: int, rows: int):
 # ----------------------------------------------------------------------------
 
 
-def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray, order: str = "mfma",
-                 k_rotation: np.ndarray | None = None) -> np.ndarray:
+def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray, order: str = "mfma") -> np.ndarray:
     """Grouped GEMM ``C[r] = A[r] @ B[e]^T`` for rows r of expert e, fp32 result.
 
     Reference ``experts.py:21-35`` with ``ENDS = offsets[1:]`` and the masked
@@ -295,11 +287,6 @@ def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray, order: str =
       GEMM outputs are one bf16 step away from this model, versus ~5e-4 for
       the exact dot product.
 
-    ``k_rotation`` (``"mfma"`` only; ``[E, N]`` ints or None): output column n
-    of expert e runs its chain over the 64-k steps starting at step
-    ``k_rotation[e, n]`` and wrapping round, as the kernels' weight-streaming
-    launches do (``decode_k_rotation``). None: ascending from step 0.
-
     Rows at or past ``offsets[E]`` are returned as 0 (undefined for the kernels).
     """
     if order not in ("mfma", "exact"):
@@ -314,34 +301,9 @@ def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray, order: str =
         be = np.asarray(b[e], dtype=np.float64)
         if order == "exact":
             out[s:t] = (a64[s:t] @ be.T).astype(np.float32)
-        elif k_rotation is None or not np.any(k_rotation[e]):
-            out[s:t] = _mfma_order_matmul(a64[s:t], be)
         else:
-            for r in np.unique(k_rotation[e]):
-                cols = np.nonzero(k_rotation[e] == r)[0]
-                shift = int(r) * 64  # step r first: roll k so that it sits at 0, a and b alike
-                out[s:t, cols] = _mfma_order_matmul(np.roll(a64[s:t], -shift, axis=1),
-                                                    np.roll(be[cols], -shift, axis=1))
+            out[s:t] = _mfma_order_matmul(a64[s:t], be)
     return out
-
-
-def decode_k_rotation(experts: int, n_out: int, k: int, gate_up: bool = False) -> np.ndarray | None:
-    """First 64-k step of each output column's MFMA chain in the kernels'
-    weight-streaming launches (``[E, columns of B]``), or None unless k/64 is a
-    power of two of at least 32 (the chains then ascend from step 0).
-
-    The kernels' own schedule, not the reference's (which leaves the fp32
-    addition order open, ``_triton_gemm.py:27-70``): column c of expert e starts
-    at step ``(7 * (c // 64) + 37 * e) mod (k / 64)``. With ``gate_up`` the
-    weight has 2 * n_out rows, and up row n_out + c shares gate row c's start
-    (one tile reads both).
-    """
-    steps = k // 64
-    if k % 64 or steps < 32 or steps & (steps - 1):
-        return None
-    cols = np.arange(n_out)
-    table = (7 * (cols[None, :] // 64) + 37 * np.arange(experts)[:, None]) % steps
-    return np.concatenate([table, table], axis=1) if gate_up else table
 
 
 def _mfma_order_matmul(a64: np.ndarray, b64: np.ndarray, group: int = 8) -> np.ndarray:

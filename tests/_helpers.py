@@ -34,26 +34,6 @@ def raw_bits(t: torch.Tensor) -> np.ndarray:
     return t.view(torch.int64).numpy()
 
 
-def gemm_k_rotation(rows: int, experts: int, n_out: int, k: int, swiglu: bool = False):
-    """The oracle ``k_rotation`` table of one grouped-GEMM launch, or None.
-
-    Mirrors the launcher (``launch_gemm_t`` in ``csrc/gemm.hip``): a launch over
-    a buffer of ``rows`` rows takes the weight-streaming kernel when k % 64 == 0
-    and rows <= 128, or rows <= 128 * E while the 256 x 256 tiles (rows spread
-    evenly over the experts) would number fewer than the CUs. That kernel
-    rotates its k chains (``oracle.decode_k_rotation``); the others ascend.
-    """
-    if k % 64:
-        return None
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    n_tiles = -(-n_out // (128 if swiglu else 256))
-    per_expert = -(-rows // experts)
-    wide_tiles = experts * -(-per_expert // 256) * n_tiles
-    if not (rows <= 128 or (rows <= 128 * experts and wide_tiles < cus)):
-        return None
-    return oracle.decode_k_rotation(experts, n_out, k, gate_up=swiglu)
-
-
 def rel_l2(got: np.ndarray, ref: np.ndarray) -> float:
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)

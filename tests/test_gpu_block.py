@@ -25,8 +25,7 @@ import torch
 
 from moe_dispatch.layer import MoEBlock, MoEConfig
 from oracle import moe_oracle as oracle
-from tests._helpers import (LazyExpertWeights, assert_near_bit_exact, gemm_k_rotation, gpu, rel_l2, route_margin,
-                            to_np)
+from tests._helpers import LazyExpertWeights, assert_near_bit_exact, gpu, rel_l2, route_margin, to_np
 
 pytestmark = gpu
 
@@ -47,12 +46,6 @@ def _run_block(cfg, tokens, pattern, seed, bias=None):
     state = block.workspace(x)
     torch.cuda.synchronize()
     return block, x, out, ids32, weights, state
-
-
-def _gemm_rotations(cfg, rows):
-    """k-chain orders of the block's gate/up and down launches over `rows` packed rows."""
-    return (gemm_k_rotation(rows, cfg.experts, cfg.intermediate, cfg.hidden, swiglu=True),
-            gemm_k_rotation(rows, cfg.experts, cfg.hidden, cfg.intermediate))
 
 
 def _check_block(cfg, tokens, pattern="balanced", seed=0, bias=None, large_i=False):
@@ -85,11 +78,10 @@ def _check_block(cfg, tokens, pattern="balanced", seed=0, bias=None, large_i=Fal
     offsets = layout["offsets"]
     # Expert GEMMs, each on the kernels' own input.
     act = to_np(state.activated)
-    rot_gu, rot_dn = _gemm_rotations(cfg, rows)
-    proj_ref = oracle.bf16_round(oracle.grouped_gemm(packed[:used], gate_up, offsets, k_rotation=rot_gu))
+    proj_ref = oracle.bf16_round(oracle.grouped_gemm(packed[:used], gate_up, offsets))
     assert_near_bit_exact(act[:used], oracle.swiglu(proj_ref, used), max_fraction=2e-4, max_steps=2.0)
     eo = to_np(state.expert_output)
-    eo_ref = oracle.bf16_round(oracle.grouped_gemm(act[:used], down, offsets, k_rotation=rot_dn))
+    eo_ref = oracle.bf16_round(oracle.grouped_gemm(act[:used], down, offsets))
     assert_near_bit_exact(eo[:used], eo_ref, max_fraction=1e-4)
     # Combine, bit-exact on the kernels' expert output.
     got = to_np(out)
@@ -292,11 +284,10 @@ def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, to
     gate_up, down = LazyExpertWeights(block.gate_up_weight), LazyExpertWeights(block.down_weight)
     packed_s = to_np(transport.packed.index_select(0, rows_t))
     act_s = to_np(state.activated.index_select(0, rows_t))
-    rot_gu, rot_dn = _gemm_rotations(cfg, transport.capacity_rows)
-    proj_ref = oracle.bf16_round(oracle.grouped_gemm(packed_s, gate_up, sample_offsets, k_rotation=rot_gu))
+    proj_ref = oracle.bf16_round(oracle.grouped_gemm(packed_s, gate_up, sample_offsets))
     assert_near_bit_exact(act_s, oracle.swiglu(proj_ref, len(rows)), max_fraction=2e-4, max_steps=2.0)
     eo_s = to_np(state.expert_output.index_select(0, rows_t))
-    eo_ref = oracle.bf16_round(oracle.grouped_gemm(act_s, down, sample_offsets, k_rotation=rot_dn))
+    eo_ref = oracle.bf16_round(oracle.grouped_gemm(act_s, down, sample_offsets))
     assert_near_bit_exact(eo_s, eo_ref, max_fraction=1e-4)
     # Combine on sampled tokens, bit-exact on the kernels' expert output.
     inv_s = layout["inverse"][tsample]

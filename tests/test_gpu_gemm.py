@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as oracle
-from tests._helpers import assert_near_bit_exact, gemm_k_rotation, gpu, rel_l2, to_np
+from tests._helpers import assert_near_bit_exact, gpu, rel_l2, to_np
 
 pytestmark = gpu
 
@@ -52,8 +52,6 @@ GEMM_CASES = [
     ([90, 20, 0], 8, 200, 128),
     ([7, 0, 40], 1, 96, 192),
     ([2, 2], 1, 4096, 1024),
-    # weight-streaming with k/64 a power of two >= 32: rotated k chains
-    ([3, 0, 1], 1, 320, 2048),
 ]
 
 
@@ -66,8 +64,7 @@ def test_grouped_gemm_matches_float64(ext, counts, alignment, n, k):
     c = torch.full((rows, n), 7.0, device="cuda").bfloat16()
     ext.grouped_gemm_out(a, b, offsets, c)
     exact = oracle.grouped_gemm(to_np(a), to_np(b), to_np(offsets), order="exact")
-    rot = gemm_k_rotation(rows, experts, n, k)
-    mfma = oracle.grouped_gemm(to_np(a), to_np(b), to_np(offsets), order="mfma", k_rotation=rot)
+    mfma = oracle.grouped_gemm(to_np(a), to_np(b), to_np(offsets), order="mfma")
     used = int(to_np(offsets)[-1])
     got = to_np(c)
     assert_near_bit_exact(got[:used], oracle.bf16_round(mfma)[:used])
@@ -140,7 +137,6 @@ GATEUP_CASES = [
     # at most 128 rows in all: the 64-column decode tiles
     ([70, 9], 8, 96, 200),
     ([2, 0, 0, 1], 1, 512, 64),
-    ([3, 1], 1, 2048, 96),  # rotated k chains (32 steps)
 ]
 
 
@@ -153,8 +149,7 @@ def test_gateup_swiglu_matches_unfused_pipeline(ext, counts, alignment, hidden, 
     act = torch.full((rows, inter), 3.0, device="cuda").bfloat16()
     ext.gateup_swiglu_out(a, w, offsets, act)
     used = int(to_np(offsets)[-1])
-    rot = gemm_k_rotation(rows, experts, inter, hidden, swiglu=True)
-    proj = oracle.bf16_round(oracle.grouped_gemm(to_np(a), to_np(w), to_np(offsets), order="mfma", k_rotation=rot))
+    proj = oracle.bf16_round(oracle.grouped_gemm(to_np(a), to_np(w), to_np(offsets), order="mfma"))
     ref = oracle.swiglu(proj, used)[:used]
     got = to_np(act)
     # A one-step flip of g or u moves silu(g)*u by up to ~2 bf16 steps.
@@ -163,18 +158,9 @@ def test_gateup_swiglu_matches_unfused_pipeline(ext, counts, alignment, hidden, 
     assert rel_l2(got[:used], exact[:used]) < 3e-3
     assert np.all(got[used:] == 3.0), "rows past offsets[E] must not be written"
     # The same kernels unfused (plain GEMM -> standalone SwiGLU): identical up to the
-    # rounding of silu's exp/reciprocal (one bf16 step, rarely) when both launches
-    # run their k chains in the same order; a weight-streaming plain launch rotates
-    # an up column by its own column block, so then each is held to its own order.
+    # rounding of silu's exp/reciprocal (one bf16 step, rarely).
     projection = torch.empty(rows, 2 * inter, device="cuda", dtype=torch.bfloat16)
     ext.grouped_gemm_out(a, w, offsets, projection)
     unfused = torch.empty_like(act)
     ext.swiglu_out(projection, offsets[-1:], unfused)
-    plain_rot = gemm_k_rotation(rows, experts, 2 * inter, hidden)
-    if rot is None and plain_rot is None:
-        assert_near_bit_exact(got[:used], to_np(unfused)[:used], max_fraction=1e-4, max_steps=1.0)
-    else:
-        plain = oracle.bf16_round(
-            oracle.grouped_gemm(to_np(a), to_np(w), to_np(offsets), order="mfma", k_rotation=plain_rot))
-        assert_near_bit_exact(to_np(projection)[:used], plain[:used])
-        assert np.array_equal(to_np(unfused)[:used], oracle.swiglu(to_np(projection), used)[:used])
+    assert_near_bit_exact(got[:used], to_np(unfused)[:used], max_fraction=1e-4, max_steps=1.0)
