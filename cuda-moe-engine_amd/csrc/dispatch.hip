@@ -84,9 +84,16 @@ __global__ __launch_bounds__(kRankThreads) void count_rank_kernel(
 // in-chunk ranks into within-expert slots and destinations, and copies each
 // token row once from x to its K destinations with VB-byte accesses. Blocks
 // e, e+grid, ... also zero the padding rows of expert e.
+//
+// The source rows do not depend on the destinations, so each thread loads its
+// first kPackEarly vectors of x before the prefix work and stores them after:
+// all blocks start together, and the prefix's dependent global reads and
+// barriers (a few microseconds) would otherwise pass with no copy traffic
+// (H=4096, 4096 tokens: 19.7 us before).
 // ---------------------------------------------------------------------------
 constexpr int kPackThreads = 256;
 constexpr int kPackMaxAssign = 256;  // pack_tokens * K upper bound
+constexpr int kPackEarly = 4;        // vectors of x per thread loaded before the prefix
 
 template <int VB> struct VecOf;
 template <> struct VecOf<16> { using T = uint4; };
@@ -128,6 +135,22 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int lane = tid % kWave;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * pack_tokens;
     const int my_chunk = static_cast<int>(t0 / chunk_tokens);
+    const int64_t t_end = min(t0 + pack_tokens, tokens);
+    const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
+    // Item i of this block is vector i % nv of token t0 + i / nv (the launcher
+    // keeps pack_tokens * nv within int32).
+    const int nv = static_cast<int>(row_bytes / VB);
+    const int items = n_tok * nv;
+    auto src = [&](int i) {
+        const int tl = i / nv;
+        return reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[i - tl * nv];
+    };
+    V early[kPackEarly];
+#pragma unroll
+    for (int j = 0; j < kPackEarly; ++j) {
+        const int i = tid + j * kPackThreads;
+        if (i < items) early[j] = src(i);
+    }
 
     if constexpr (COUNT) {
         // (a') Every assignment in rounds of kPackThreads: totals in `total`, and
@@ -228,8 +251,6 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     }
 
     // (b) Destinations of this block's assignments.
-    const int64_t t_end = min(t0 + pack_tokens, tokens);
-    const int n_tok = static_cast<int>(max<int64_t>(t_end - t0, 0));
     const int n_local = n_tok * topk;
     for (int i = tid; i < n_local; i += kPackThreads) {
         const int64_t p = t0 * topk + i;
@@ -251,17 +272,20 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     __syncthreads();
 
     // (c) Row copies: each x row is read once and written to its K rows.
-    const int64_t nv = row_bytes / VB;
-    const int64_t items = static_cast<int64_t>(n_tok) * nv;
-    for (int64_t i = tid; i < items; i += kPackThreads) {
-        const int tl = static_cast<int>(i / nv);
-        const int64_t v = i - static_cast<int64_t>(tl) * nv;
-        const V val = reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[v];
+    auto store = [&](int i, const V& val) {
+        const int tl = i / nv;
+        const int v = i - tl * nv;
         for (int k = 0; k < topk; ++k) {
             const int64_t d = dest[tl * topk + k];
             if (d >= 0) reinterpret_cast<V*>(packed + d * row_bytes)[v] = val;
         }
+    };
+#pragma unroll
+    for (int j = 0; j < kPackEarly; ++j) {
+        const int i = tid + j * kPackThreads;
+        if (i < items) store(i, early[j]);
     }
+    for (int i = tid + kPackEarly * kPackThreads; i < items; i += kPackThreads) store(i, src(i));
 
     // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
     for (int e = blockIdx.x; e < experts; e += gridDim.x) {
@@ -423,18 +447,20 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
     const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes);
     const int64_t n_assign = tokens * topk;
     const bool count_in_pack = n_assign <= kSmallAssign;
+    int vb = static_cast<int>(elem);
+    if (vectorized) {
+        if (row_bytes % 16 == 0) vb = 16;
+        else if (row_bytes % 8 == 0) vb = 8;
+        else if (row_bytes % 4 == 0) vb = 4;
+    }
+    MOE_REQUIRE(plan.pack_tokens * (row_bytes / vb) <= INT32_MAX, MOE_ERR_UNSUPPORTED,
+                "row of %lld bytes too large for the pack kernel", (long long)row_bytes);
     if (plan.n_chunks > 0 && !count_in_pack) {
         hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)),
                            dim3(kRankThreads), 0, stream, ids, slots, chunk_counts, n_assign,
                            experts, plan.chunk_tokens * topk);
         int rc = check_launch("count_rank_kernel");
         if (rc != MOE_OK) return rc;
-    }
-    int vb = static_cast<int>(elem);
-    if (vectorized) {
-        if (row_bytes % 16 == 0) vb = 16;
-        else if (row_bytes % 8 == 0) vb = 8;
-        else if (row_bytes % 4 == 0) vb = 4;
     }
     const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
     const dim3 grid(static_cast<unsigned>(plan.pack_blocks));
