@@ -151,6 +151,16 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
         const int i = tid + j * kPackThreads;
         if (i < items) early[j] = src(i);
     }
+    // This thread's assignment (n_tok * K <= kPackMaxAssign == kPackThreads):
+    // its expert and in-chunk rank do not depend on the prefix either.
+    static_assert(kPackMaxAssign <= kPackThreads, "one assignment per thread");
+    const int n_local = n_tok * topk;
+    const int64_t my_p = t0 * topk + tid;
+    const int my_e = tid < n_local ? ids[my_p] : -1;
+    int my_rank = -1;
+    if constexpr (!COUNT) {
+        if (tid < n_local) my_rank = slots[my_p];
+    }
 
     if constexpr (COUNT) {
         // (a') Every assignment in rounds of kPackThreads: totals in `total`, and
@@ -251,23 +261,21 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     }
 
     // (b) Destinations of this block's assignments.
-    const int n_local = n_tok * topk;
-    for (int i = tid; i < n_local; i += kPackThreads) {
-        const int64_t p = t0 * topk + i;
-        const int e = ids[p];
+    if (tid < n_local) {
+        const int e = my_e;
         int64_t d = -1;
         if (e >= 0 && e < experts) {
-            const int r = COUNT ? own_rank[i] : slots[p];
+            const int r = COUNT ? own_rank[tid] : my_rank;
             if (r >= 0) {
                 const int slot = before[e] + r;
                 d = static_cast<int64_t>(offs[e]) + slot;
-                slots[p] = slot;
-                inverse[p] = static_cast<int32_t>(d);
+                slots[my_p] = slot;
+                inverse[my_p] = static_cast<int32_t>(d);
             }
         } else if constexpr (COUNT) {
-            slots[p] = -1;  // (count_rank_kernel writes this on the other path)
+            slots[my_p] = -1;  // (count_rank_kernel writes this on the other path)
         }
-        dest[i] = d;
+        dest[tid] = d;
     }
     __syncthreads();
 
