@@ -692,23 +692,28 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
 //
 // For the plain GEMM a short last round (at most half of the slots busy) of
 // phase 1 (when there is no phase 2) or of the leftover phase-2 tiles is split
-// into 128-column pieces. Every tile or piece runs its whole k chain in order
+// into 128-column pieces, and leftover phase-2 tiles into 64-column quarters
+// when at most a quarter of the slots would be busy. Every tile or piece runs its whole k chain in order
 // on one workgroup, so results do not depend on the schedule or on G.
 struct RingPhase {
     int count;   // tiles
     int main;    // tiles mapped XCD-contiguously
     int blocks;  // virtual workgroups of the main part (multiple of 8)
-    int pieces;  // split tail pieces (2 per split tile)
+    int pieces;  // split tail pieces (`ways` per split tile)
+    int ways;    // 2 (128-column pieces) or 4 (64-column pieces of short tiles)
 };
 
-__device__ __forceinline__ RingPhase ring_phase(int count, int grid, bool allow_split) {
+// Short tiles (phase 2) split four ways when that still fits the slots: their
+// cost is streaming the weight slab, which more CUs pull faster.
+__device__ __forceinline__ RingPhase ring_phase(int count, int grid, bool allow_split, bool short_tiles) {
     RingPhase ph;
     ph.count = count;
     const int rem = count % grid;
     const bool split = allow_split && rem > 0 && 2 * rem <= grid;
+    ph.ways = short_tiles && 4 * rem <= grid ? 4 : 2;
     ph.main = split ? count - rem : count;
     ph.blocks = (ph.main + kNumXcd - 1) / kNumXcd * kNumXcd;
-    ph.pieces = split ? 2 * rem : 0;
+    ph.pieces = split ? ph.ways * rem : 0;
     return ph;
 }
 
@@ -742,7 +747,7 @@ __device__ __forceinline__ RingPlan ring_plan(int n1, int n2, int grid, bool all
         pl.slots = rounds * grid - kNumXcd * pl.per1;
         pl.carried = min(n2, 2 * pl.slots);
     }
-    pl.rest = ring_phase(n2 > 0 ? n2 - pl.carried : n1, grid, allow_split);
+    pl.rest = ring_phase(n2 > 0 ? n2 - pl.carried : n1, grid, allow_split, n2 > 0);
     pl.virtual_blocks = pl.rounds * grid + pl.rest.blocks + pl.rest.pieces;
     return pl;
 }
@@ -750,7 +755,7 @@ __device__ __forceinline__ RingPlan ring_plan(int n1, int n2, int grid, bool all
 struct RingSlot {
     int phase;  // 0 / 1 for phase 1 / 2; -1: no tile
     int tile;   // index inside the phase of the first tile
-    int piece;  // -1, or 0 / 1 for the two 128-column halves
+    int piece;  // -1; 0 / 1 for the two 128-column halves; 4 + q for 64-column quarter q
     int count;  // tiles tile, tile + 1, ... of this slot (0 to 2)
 };
 
@@ -792,7 +797,7 @@ __device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int 
         if (tile < ph.main) s = RingSlot{phase, first + tile, -1, 1};
     } else if (v - ph.blocks < ph.pieces) {
         const int r = v - ph.blocks;
-        s = RingSlot{phase, first + ph.main + r / 2, r % 2, 1};
+        s = RingSlot{phase, first + ph.main + r / ph.ways, ph.ways == 4 ? 4 + r % 4 : r % 2, 1};
     }
     return s;
 }
@@ -807,7 +812,7 @@ __device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int 
 struct RingWork {
     bool valid;
     int expert;
-    int variant;  // row tile 256 / 128 / 64 = 0 / 1 / 2; +3 for a 128-column piece
+    int variant;  // row tile 256 / 128 / 64 = 0 / 1 / 2; +3 for a 128-column piece, +6 for a 64-column one
     int64_t row0, row_end, col0;
 };
 
@@ -880,9 +885,12 @@ __device__ __forceinline__ RingWork ring_locate(const GemmParams& p, const RingT
         w.col0 = static_cast<int64_t>(n_tile) * 128;
     } else if (s.piece < 0) {
         w.col0 = static_cast<int64_t>(n_tile) * 256;
-    } else {
+    } else if (s.piece < 4) {
         w.col0 = static_cast<int64_t>(n_tile) * 256 + s.piece * 128;
         w.variant += 3;
+    } else {
+        w.col0 = static_cast<int64_t>(n_tile) * 256 + (s.piece - 4) * 64;
+        w.variant += 6;
     }
     w.expert = e;
     w.valid = true;
@@ -901,7 +909,10 @@ __device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, co
             if constexpr (!SWIGLU) {
                 if (w.variant == 3) go(RingOps<4, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
                 else if (w.variant == 4) go(RingOps<2, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
-                else go(RingOps<1, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else if (w.variant == 5) go(RingOps<1, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else if (w.variant == 6) go(RingOps<4, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else if (w.variant == 7) go(RingOps<2, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else go(RingOps<1, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
             }
     }
 }
@@ -919,8 +930,14 @@ __device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const R
                     ring_tile<4, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
                 else if (w.variant == 4)
                     ring_tile<2, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
-                else
+                else if (w.variant == 5)
                     ring_tile<1, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
+                else if (w.variant == 6)
+                    ring_tile<4, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
+                else if (w.variant == 7)
+                    ring_tile<2, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
+                else
+                    ring_tile<1, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
             }
     }
 }

@@ -29,11 +29,13 @@ def phase_counts(counts, alignment, n_tiles):
     return n1, n2
 
 
-def ring_phase(count, grid, allow_split):
+def ring_phase(count, grid, allow_split, short_tiles=False):
     rem = count % grid
     split = allow_split and rem > 0 and 2 * rem <= grid
+    ways = 4 if short_tiles and 4 * rem <= grid else 2
     main = count - rem if split else count
-    return {"main": main, "blocks": (main + XCD - 1) // XCD * XCD, "pieces": 2 * rem if split else 0}
+    return {"main": main, "blocks": (main + XCD - 1) // XCD * XCD, "pieces": ways * rem if split else 0,
+            "ways": ways}
 
 
 def ring_plan(n1, n2, grid, allow_split):
@@ -48,7 +50,7 @@ def ring_plan(n1, n2, grid, allow_split):
         slots = rounds * grid - XCD * per1
         pl.update(per1=per1, rounds=rounds, cpr=cpr, full_rounds=per1 // cpr,
                   last_cols=per1 - (per1 // cpr) * cpr, slots=slots, carried=min(n2, 2 * slots))
-    pl["rest"] = ring_phase(n2 - pl["carried"] if n2 > 0 else n1, grid, allow_split)
+    pl["rest"] = ring_phase(n2 - pl["carried"] if n2 > 0 else n1, grid, allow_split, n2 > 0)
     pl["virtual_blocks"] = pl["rounds"] * grid + pl["rest"]["blocks"] + pl["rest"]["pieces"]
     return pl
 
@@ -84,7 +86,8 @@ def ring_slot(pl, grid, q, sub):
         return (phase, first + tile, -1) if tile < rest["main"] else None
     if v - rest["blocks"] < rest["pieces"]:
         r = v - rest["blocks"]
-        return (phase, first + rest["main"] + r // 2, r % 2)
+        ways = rest["ways"]
+        return (phase, first + rest["main"] + r // ways, 4 + r % 4 if ways == 4 else r % 2)
     return None
 
 
@@ -115,7 +118,9 @@ def check_cover(n1, n2, grid, allow_split):
     for phase, tile, piece in seen:
         parts.setdefault((phase, tile), set()).add(piece)
     assert set(parts) == {(0, t) for t in range(n1)} | {(1, t) for t in range(n2)}
-    assert all(p in ({-1}, {0, 1}) for p in parts.values())
+    assert all(p in ({-1}, {0, 1}, {4, 5, 6, 7}) for p in parts.values())
+    # Quarters only for short tiles (phase 2), halves for either phase.
+    assert all(phase == 1 for (phase, _), p in parts.items() if p == {4, 5, 6, 7})
     assert not (pl["carried"] and not allow_split and pl["rest"]["pieces"])
     # In the rounds, the workgroups of XCD x (those with blockIdx % 8 == x) run
     # exactly phase-1 range x, each round's tiles before the next round's.
@@ -157,13 +162,13 @@ def test_grid_sizes_used_on_the_gpu_cover_each_path():
             if pl["carried"] and pl["carried"] < n2:
                 reached.add("leftover after the rounds")
             if pl["rest"]["pieces"]:
-                reached.add("pieces")
+                reached.add("quarters" if pl["rest"]["ways"] == 4 else "pieces")
             if pl["rounds"] and pl["last_cols"]:
                 reached.add("partial last round")
             if pl["rounds"] > (pl["per1"] + grid // XCD - 1) // (grid // XCD):
                 reached.add("extra round")
-    assert reached == {"two tiles in a slot", "leftover after the rounds", "pieces", "partial last round",
-                       "extra round"}
+    assert reached == {"two tiles in a slot", "leftover after the rounds", "pieces", "quarters",
+                       "partial last round", "extra round"}
 
 
 def test_phase2_slots_rotate_over_the_cus():
@@ -181,9 +186,9 @@ def test_measured_shapes_get_the_intended_plans():
     pl = ring_plan(*phase_counts(c4, 8, 112), 256, False)
     assert (pl["rounds"], pl["cpr"], pl["carried"], pl["n2"]) == (15, 30, 448, 448)
     # Its down GEMM (512 full tiles = 2 rounds, 64 short tiles): no extra round;
-    # the short tiles run last as 128 split pieces.
+    # the short tiles run last as 256 quarters, one per workgroup.
     pl = ring_plan(*phase_counts(c4, 8, 16), 256, True)
-    assert (pl["rounds"], pl["carried"], pl["rest"]["pieces"]) == (2, 0, 128)
+    assert (pl["rounds"], pl["carried"], pl["rest"]["pieces"], pl["rest"]["ways"]) == (2, 0, 256, 4)
     # No short tiles: phase 1 alone, as before.
     pl = ring_plan(*phase_counts([1024] * 8, 8, 112), 256, False)
     assert (pl["rounds"], pl["rest"]["blocks"]) == (0, 3584)
