@@ -9,7 +9,8 @@ Prints ONE JSON line: value = mean forward latency (us) over the timed steps,
 plus per-stage latencies, expert-GEMM TFLOP/s, dispatch/combine GB/s, the
 roofline of the dominant kernel (gate/up GEMM with the SwiGLU epilogue, timed
 with events on the stream it is launched on), the PyTorch variant on the same
-GPU, and a CPU baseline (the oracle on a bounded token sample, rank 0 only).
+GPU, and a CPU baseline: the same PyTorch variant on the host CPU at BASELINE
+config 1 (all cores and one thread), plus a token sample of this workload.
 """
 
 from __future__ import annotations
@@ -46,6 +47,20 @@ TRANSPORT_CONFIGS = {"c2_transport": (4096, 2048, 8, 2, 1)}
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
 
 
+def dispatch_bytes(tokens, hidden, topk, padding_rows, elem=2):
+    """Algorithmic dispatch bytes: x read once, each assignment's row and the
+    padding rows written once, the ids read and the inverse map written (4 B each)."""
+    n = tokens * topk
+    return (tokens + n + padding_rows) * hidden * elem + n * 8
+
+
+def combine_bytes(tokens, hidden, topk, elem=2):
+    """Algorithmic combine bytes: K rows gathered per token, one row written, the
+    inverse map and the weights read (4 B each)."""
+    n = tokens * topk
+    return (n + tokens) * hidden * elem + n * 8
+
+
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -59,7 +74,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch-variant", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replay timing")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=2048)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=64,
+                    help="tokens of the benchmark workload the CPU variant also runs (0: config 1 only)")
     return ap.parse_args(argv)
 
 
@@ -108,54 +124,106 @@ def time_stages(block, x, steps, warmup):
         return {name: {"mean_us": time_loop(fn, steps, warmup)} for name, fn in stages.items()}
 
 
-def cpu_baseline(block, x, sample_tokens):
-    """The CPU oracle on `sample_tokens` tokens of the same workload; scaled to a full forward."""
-    import numpy as np
-
-    from oracle import moe_oracle as oracle
-
+def _cpu_model():
     try:
-        from threadpoolctl import threadpool_info
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:  # pragma: no cover
+        pass
+    import platform
 
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    tokens = x.shape[0]
-    sample = x[:sample_tokens].float().cpu().numpy()
-    router = block.router_weight.cpu().numpy()
-    bias = block.routing_bias.cpu().numpy()
-    cfg = block.config
-    t0 = time.perf_counter()
-    logits = oracle.router_logits(sample, router)
-    ids, weights, _ = oracle.topk_route(logits, bias, cfg.topk)
-    used = sorted(set(ids.reshape(-1).tolist()))
-    gate_up = {e: block.gate_up_weight[e].float().cpu().numpy() for e in used}
-    down = {e: block.down_weight[e].float().cpu().numpy() for e in used}
-    convert_s = time.perf_counter() - t0
+    return platform.processor() or "unknown"
 
-    class _W:
-        def __init__(self, d, shape):
-            self.d, self.shape = d, shape
 
-        def __getitem__(self, e):
-            return self.d[e]
+def _host_threads():
+    """CPUs this process may run on (the box's share, not the whole host), capped by OMP_NUM_THREADS."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        avail = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return min(avail, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else avail
 
-    gu_w = _W(gate_up, tuple(block.gate_up_weight.shape))
-    dn_w = _W(down, tuple(block.down_weight.shape))
-    # Untimed warm-up on two tokens (first touch of the weight pages, BLAS start-up).
-    oracle.token_major_forward(sample[:2], gu_w, dn_w, ids[:2], weights[:2])
-    t1 = time.perf_counter()
-    oracle.token_major_forward(sample, gu_w, dn_w, ids, weights)
-    compute_s = time.perf_counter() - t1 + (t1 - t0 - convert_s)
-    per_token_us = compute_s * 1e6 / sample_tokens
-    return {
-        "value": per_token_us * tokens,
-        "unit": "us",
-        "cores": int(threads),
-        "kind": "port",
-        "sample": f"{sample_tokens} of {tokens} tokens through the numpy oracle (router, top-k, "
-                  f"per-expert float64 GEMMs, SwiGLU, combine); {compute_s:.2f} s, scaled x{tokens / sample_tokens:.0f}",
-    }
+
+def _time_cpu(fn, warmup, samples):
+    """perf_counter_ns around each call after `warmup` untimed calls: median/p95/min in us."""
+    from moe_dispatch.evidence import percentile
+
+    for _ in range(warmup):
+        fn()
+    values = []
+    for _ in range(samples):
+        t0 = time.perf_counter_ns()
+        fn()
+        values.append((time.perf_counter_ns() - t0) / 1000.0)
+    return {"median_us": round(statistics.median(values), 2), "p95_us": round(percentile(values, 0.95), 2),
+            "min_us": round(min(values), 2), "samples": samples, "warmup": warmup}
+
+
+def cpu_baseline(gpu_block=None, gpu_x=None, c4_sample_tokens=64):
+    """The PyTorch variant (implementation="torch", F.grouped_mm) on the host CPU.
+
+    Main figure: BASELINE config 1 (T=128, H=512, I=1024, E=8, top-2, bf16, seed 0),
+    every token, 10 warm-ups + 40 perf_counter_ns samples, with all the CPUs this
+    process may use and again with 1 thread. When the benchmark's own block is
+    given, the same variant also runs on its first `c4_sample_tokens` tokens with
+    its weights (copied to the host), reported per token and scaled to the full
+    token count (labelled as such: the weights are streamed once per call, so a
+    small sample over-weights that cost).
+    """
+    import torch
+
+    from moe_dispatch.layer import MoEBlock, MoEConfig, make_weights
+
+    threads_before = torch.get_num_threads()
+    threads = _host_threads()
+    cfg = MoEConfig(512, 1024, 8, 2)
+    weights = make_weights(cfg, "cpu", torch.bfloat16, seed=0)
+    block = MoEBlock(cfg, device="cpu", dtype=torch.bfloat16, implementation="torch", weights=weights)
+    x = torch.randn(128, 512, generator=torch.Generator().manual_seed(0)).bfloat16()
+    runs = {}
+    try:
+        for label, n in (("all_cores", threads), ("one_thread", 1)):
+            torch.set_num_threads(n)
+            runs[label] = {"threads": n, **_time_cpu(lambda: block(x), 10, 40)}
+        result = {
+            "value": runs["all_cores"]["median_us"],
+            "unit": "us",
+            "cores": threads,
+            "kind": "port",
+            "sample": "this repo's PyTorch variant of the reference block (implementation='torch': topk/softmax "
+                      "router, stable-sort transport, F.grouped_mm experts, fp32 combine) at BASELINE config 1 "
+                      "(T=128 H=512 I=1024 E=8 top-2 bf16, seed 0), all 128 tokens, no scaling; median of 40 "
+                      "perf_counter_ns samples after 10 warm-ups",
+            "config": {"tokens": 128, "hidden": 512, "intermediate": 1024, "experts": 8, "topk": 2,
+                       "dtype": "bf16"},
+            "all_cores": runs["all_cores"],
+            "one_thread": runs["one_thread"],
+            "cpu_model": _cpu_model(),
+            "host_cpu_count": os.cpu_count(),
+            "torch_version": torch.__version__,
+        }
+        if gpu_block is not None and c4_sample_tokens > 0:
+            torch.set_num_threads(threads)
+            bcfg = gpu_block.config
+            host_w = type(weights)(gpu_block.router_weight.cpu(), gpu_block.gate_up_weight.cpu(),
+                                   gpu_block.down_weight.cpu())
+            host = MoEBlock(bcfg, device="cpu", dtype=torch.bfloat16, implementation="torch", weights=host_w)
+            host.routing_bias.copy_(gpu_block.routing_bias.cpu())
+            xs = gpu_x[:c4_sample_tokens].cpu()
+            timing = _time_cpu(lambda: host(xs), 1, 3)
+            total = gpu_x.shape[0]
+            result["bench_workload_sample"] = {
+                "tokens": c4_sample_tokens, "of_tokens": total, "threads": threads, **timing,
+                "scaled_us": round(timing["median_us"] * total / c4_sample_tokens, 1),
+                "note": "same variant on the first tokens of the benchmark workload, median scaled linearly "
+                        "to the full token count",
+            }
+            del host, host_w
+        return result
+    finally:
+        torch.set_num_threads(threads_before)
 
 
 def torch_variant_gpu(cfg, weights, x, steps, warmup):
@@ -259,8 +327,6 @@ def transport_bench(args):
 
     from moe_dispatch.routing import make_transport_case
     from moe_dispatch.workspace import CudaWorkspace
-    from oracle import moe_oracle as oracle
-
     tokens, hidden, experts, topk, alignment = TRANSPORT_CONFIGS[args.config]
     torch.cuda.set_device(0)
     x, ids32, ids64, weights = make_transport_case(tokens, hidden, experts, topk, torch.bfloat16, seed=0)
@@ -284,8 +350,8 @@ def transport_bench(args):
         c_us = time_loop(lambda: ws.combine(y, weights), args.steps, args.warmup)
     mean_us = start.elapsed_time(end) * 1000.0 / args.steps
     pad_rows = int(ws.offsets[-1].item()) - tokens * topk
-    disp_bytes = oracle.dispatch_bytes(tokens, hidden, topk, pad_rows)
-    comb_bytes = oracle.combine_bytes(tokens, hidden, topk)
+    disp_bytes = dispatch_bytes(tokens, hidden, topk, pad_rows)
+    comb_bytes = combine_bytes(tokens, hidden, topk)
     d_gbs = disp_bytes / (d_us * 1e-6) / 1e9
     c_gbs = comb_bytes / (c_us * 1e-6) / 1e9
     traffic = measured_traffic(args.config, ("count_rank_kernel", "pack_kernel<16, false>"))
@@ -338,8 +404,8 @@ def main(argv=None):
     import numpy as np
     import torch
 
-    from moe_dispatch.layer import MoEBlock, MoEConfig, MoEWeights, make_weights
-    from oracle import moe_oracle as oracle
+    from moe_dispatch.layer import MoEBlock, MoEConfig, make_weights
+    from moe_dispatch.routing import zipf_bias
 
     tokens, hidden, inter, experts, topk, pattern = CONFIGS[args.config]
     device = torch.device("cuda", 0)
@@ -348,7 +414,7 @@ def main(argv=None):
     weights = make_weights(cfg, device, torch.bfloat16, seed=0)
     block = MoEBlock(cfg, device=device, implementation="cuda_fused", weights=weights)
     if pattern == "zipf":
-        block.set_routing_bias(torch.from_numpy(oracle.zipf_bias(experts)))
+        block.set_routing_bias(zipf_bias(experts))
     gen = torch.Generator(device=device).manual_seed(0)
     x = torch.randn(tokens, hidden, device=device, generator=gen).bfloat16()
 
@@ -385,8 +451,8 @@ def main(argv=None):
     t_gu = stages["gateup_swiglu"]["mean_us"]
     t_dn = stages["down"]["mean_us"]
     expert_tflops = (gateup_flop + down_flop) / ((t_gu + t_dn) * 1e-6) / 1e12
-    disp_bytes = oracle.dispatch_bytes(tokens, hidden, topk, pad_rows)
-    comb_bytes = oracle.combine_bytes(tokens, hidden, topk)
+    disp_bytes = dispatch_bytes(tokens, hidden, topk, pad_rows)
+    comb_bytes = combine_bytes(tokens, hidden, topk)
 
     result = {
         "metric": "MoE block fwd latency (us) + expert TFLOP/s % bf16 MFMA peak; dispatch GB/s",

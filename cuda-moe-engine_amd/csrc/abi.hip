@@ -54,6 +54,12 @@ static bool valid_dtype(int dtype) {
     return dtype == MOE_DTYPE_F32 || dtype == MOE_DTYPE_F16 || dtype == MOE_DTYPE_BF16;
 }
 
+// True when p is a multiple of `bytes` (a null pointer counts as aligned: the
+// null checks report it).
+static bool aligned_to(const void* p, uintptr_t bytes) {
+    return reinterpret_cast<uintptr_t>(p) % bytes == 0;
+}
+
 static int64_t aligned_capacity(int64_t n, int64_t experts, int64_t alignment) {
     if (alignment == 1) return n;
     return (n + experts * (alignment - 1) + 1 + alignment - 1) / alignment * alignment;
@@ -91,6 +97,9 @@ int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64
     MOE_REQUIRE(tokens <= INT_MAX / experts, MOE_ERR_CAPACITY, "tokens*experts exceeds int32");
     if (tokens == 0) return MOE_OK;
     MOE_REQUIRE(logits && bias && ids32 && weights, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(aligned_to(logits, 4) && aligned_to(bias, 4) && aligned_to(ids32, 4) &&
+                    aligned_to(weights, 4) && aligned_to(ids64, 8),
+                MOE_ERR_INVALID_ARGUMENT, "pointers must be aligned to their element size");
     return launch_topk_route(logits, bias, ids32, ids64, weights, tokens, (int)experts, (int)topk,
                              static_cast<hipStream_t>(stream));
 }
@@ -118,8 +127,12 @@ int moe_router_fused(const void* x, const float* router_w, const float* bias, in
     const int64_t need = router_scratch_bytes(experts, hidden);
     MOE_REQUIRE(scratch && scratch_bytes >= need, MOE_ERR_WORKSPACE,
                 "router scratch needs %lld bytes, got %lld", (long long)need, (long long)scratch_bytes);
-    MOE_REQUIRE(reinterpret_cast<uintptr_t>(scratch) % 16 == 0 && reinterpret_cast<uintptr_t>(router_w) % 16 == 0,
-                MOE_ERR_INVALID_ARGUMENT, "router weights and scratch must be 16-byte aligned");
+    // x, the weights and the scratch planes are read with 16-byte (direct-to-LDS) loads.
+    MOE_REQUIRE(aligned_to(x, 16) && aligned_to(scratch, 16) && aligned_to(router_w, 16),
+                MOE_ERR_INVALID_ARGUMENT, "x, router weights and scratch must be 16-byte aligned");
+    MOE_REQUIRE(aligned_to(bias, 4) && aligned_to(ids32, 4) && aligned_to(weights, 4) &&
+                    aligned_to(logits_out, 4) && aligned_to(ids64, 8),
+                MOE_ERR_INVALID_ARGUMENT, "pointers must be aligned to their element size");
     return launch_router_fused(static_cast<const uint16_t*>(x), router_w, bias, ids32, ids64,
                                weights, logits_out, static_cast<uint16_t*>(scratch), tokens,
                                (int)hidden, (int)experts, (int)topk, static_cast<hipStream_t>(stream));
@@ -154,6 +167,14 @@ int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, 
     MOE_REQUIRE(counts && offsets && scratch, MOE_ERR_INVALID_ARGUMENT, "null pointer");
     MOE_REQUIRE(n == 0 || (x && ids && slots && packed && inverse), MOE_ERR_INVALID_ARGUMENT,
                 "null pointer");
+    // Rows are copied with the widest access that the row size and both base
+    // addresses allow (launch_dispatch), down to one element.
+    const uintptr_t elem = static_cast<uintptr_t>(dtype_size(dtype));
+    MOE_REQUIRE(aligned_to(x, elem) && aligned_to(packed, elem), MOE_ERR_INVALID_ARGUMENT,
+                "x and packed must be aligned to their element size");
+    MOE_REQUIRE(aligned_to(ids, 4) && aligned_to(counts, 4) && aligned_to(offsets, 4) &&
+                    aligned_to(slots, 4) && aligned_to(inverse, 4) && aligned_to(scratch, 4),
+                MOE_ERR_INVALID_ARGUMENT, "index buffers must be 4-byte aligned");
     return launch_dispatch(x, dtype, ids, counts, offsets, slots, packed, inverse,
                            static_cast<int32_t*>(scratch), tokens, hidden, (int)experts, (int)topk,
                            (int)alignment, vectorized != 0, static_cast<hipStream_t>(stream));
@@ -170,6 +191,12 @@ int moe_combine(const void* expert_output, int dtype, const int32_t* inverse,
     MOE_REQUIRE(packed_rows >= tokens * topk, MOE_ERR_INVALID_ARGUMENT, "shape/dtype mismatch");
     if (tokens == 0) return MOE_OK;
     MOE_REQUIRE(expert_output && inverse && weights && output, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    // 16-byte vectors when both row arrays allow them (launch_combine), else elements.
+    const uintptr_t elem = static_cast<uintptr_t>(dtype_size(dtype));
+    MOE_REQUIRE(aligned_to(expert_output, elem) && aligned_to(output, elem), MOE_ERR_INVALID_ARGUMENT,
+                "expert output and output must be aligned to their element size");
+    MOE_REQUIRE(aligned_to(inverse, 4) && aligned_to(weights, 4), MOE_ERR_INVALID_ARGUMENT,
+                "inverse and weights must be 4-byte aligned");
     return launch_combine(expert_output, dtype, inverse, weights, output, tokens, hidden,
                           (int)topk, packed_rows, static_cast<hipStream_t>(stream));
 }
@@ -181,6 +208,9 @@ int moe_swiglu(const void* projection, int dtype, const int32_t* valid_rows, voi
                 "shape exceeds index capacity");
     if (rows * width == 0) return MOE_OK;
     MOE_REQUIRE(projection && valid_rows && output, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    const uintptr_t elem = static_cast<uintptr_t>(dtype_size(dtype));
+    MOE_REQUIRE(aligned_to(projection, elem) && aligned_to(output, elem) && aligned_to(valid_rows, 4),
+                MOE_ERR_INVALID_ARGUMENT, "pointers must be aligned to their element size");
     return launch_swiglu(projection, dtype, valid_rows, output, rows, width,
                          static_cast<hipStream_t>(stream));
 }
@@ -196,6 +226,9 @@ int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offse
                 MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
     if (rows == 0) return MOE_OK;
     MOE_REQUIRE(a && b && c && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    // Operands are read with 16-byte buffer loads and results stored 8 bytes at a time.
+    MOE_REQUIRE(aligned_to(a, 16) && aligned_to(b, 16) && aligned_to(c, 16) && aligned_to(offsets, 4),
+                MOE_ERR_INVALID_ARGUMENT, "a, b and c must be 16-byte aligned (offsets 4-byte)");
     return launch_grouped_gemm(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
                                static_cast<uint16_t*>(c), offsets, rows, n, k, (int)experts,
                                static_cast<hipStream_t>(stream));
@@ -213,6 +246,8 @@ int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
                 MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
     if (rows == 0) return MOE_OK;
     MOE_REQUIRE(a && gate_up && act && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(aligned_to(a, 16) && aligned_to(gate_up, 16) && aligned_to(act, 16) && aligned_to(offsets, 4),
+                MOE_ERR_INVALID_ARGUMENT, "a, gate_up and act must be 16-byte aligned (offsets 4-byte)");
     return launch_gateup_swiglu(static_cast<const uint16_t*>(a),
                                 static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(act),
                                 offsets, rows, hidden, intermediate, (int)experts,

@@ -455,11 +455,18 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
     const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes);
     const int64_t n_assign = tokens * topk;
     const bool count_in_pack = n_assign <= kSmallAssign;
+    // The widest access that divides the row size and both base addresses (an
+    // offset view of a larger tensor may start at any element).
     int vb = static_cast<int>(elem);
     if (vectorized) {
-        if (row_bytes % 16 == 0) vb = 16;
-        else if (row_bytes % 8 == 0) vb = 8;
-        else if (row_bytes % 4 == 0) vb = 4;
+        const uint64_t bits = static_cast<uint64_t>(row_bytes) | reinterpret_cast<uintptr_t>(x) |
+                              reinterpret_cast<uintptr_t>(packed);
+        for (int w : {16, 8, 4}) {
+            if (w > vb && bits % w == 0) {
+                vb = w;
+                break;
+            }
+        }
     }
     MOE_REQUIRE(plan.pack_tokens * (row_bytes / vb) <= INT32_MAX, MOE_ERR_UNSUPPORTED,
                 "row of %lld bytes too large for the pack kernel", (long long)row_bytes);
@@ -512,17 +519,19 @@ int launch_combine(const void* y, int dtype, const int32_t* inverse, const float
                    void* out, int64_t tokens, int64_t hidden, int topk, int64_t rows,
                    hipStream_t stream) {
     if (tokens == 0) return MOE_OK;
+    // 16-byte vectors need both row arrays 16-byte aligned (rows then are too).
+    const bool vec_ok = (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out)) % 16 == 0;
     switch (dtype) {
         case MOE_DTYPE_BF16:
-            if (hidden % 8 == 0) launch_combine_t<MOE_DTYPE_BF16, 8>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            if (vec_ok && hidden % 8 == 0) launch_combine_t<MOE_DTYPE_BF16, 8>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
             else launch_combine_t<MOE_DTYPE_BF16, 1>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
             break;
         case MOE_DTYPE_F16:
-            if (hidden % 8 == 0) launch_combine_t<MOE_DTYPE_F16, 8>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            if (vec_ok && hidden % 8 == 0) launch_combine_t<MOE_DTYPE_F16, 8>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
             else launch_combine_t<MOE_DTYPE_F16, 1>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
             break;
         case MOE_DTYPE_F32:
-            if (hidden % 4 == 0) launch_combine_t<MOE_DTYPE_F32, 4>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
+            if (vec_ok && hidden % 4 == 0) launch_combine_t<MOE_DTYPE_F32, 4>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
             else launch_combine_t<MOE_DTYPE_F32, 1>(y, inverse, weights, out, tokens, hidden, topk, rows, stream);
             break;
         default: return fail(MOE_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);

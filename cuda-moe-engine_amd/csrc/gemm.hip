@@ -1198,6 +1198,10 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
                            dim3(kRingThreads), 0, stream, p);
         return check_launch("grouped_gemm_persistent_kernel");
     }
+    // The generic kernel maps workgroup b to tile (b % 8) * per_xcd + b / 8 with
+    // per_xcd = ceil(tiles / 8), which reaches every tile only when the grid
+    // holds all 8 * per_xcd slots: round the upper bound up to a multiple of 8.
+    blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
     if (blocks > INT32_MAX) return fail(MOE_ERR_CAPACITY, "grouped GEMM grid too large");
     hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, SWIGLU>),
                        dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads), 0, stream, p);

@@ -18,11 +18,12 @@ import torch
 
 from . import _lib
 
-_DTYPES = {
+DTYPE_CODES = {
     torch.float32: _lib.DTYPE_F32,
     torch.float16: _lib.DTYPE_F16,
     torch.bfloat16: _lib.DTYPE_BF16,
 }
+_DTYPES = DTYPE_CODES
 
 
 def _check(condition, message):
@@ -37,8 +38,17 @@ def _check_gpu_tensor(tensor, anchor, name):
     _check(tensor.device == anchor.device, f"{name}: device mismatch")
 
 
+def current_stream_handle(device_index):
+    """The current torch stream's HIP handle on a device (torch's raw accessor when it has one)."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(device_index)
+    return torch.cuda.current_stream(device_index).cuda_stream
+
+
 def _stream(device):
-    return torch.cuda.current_stream(device).cuda_stream
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return current_stream_handle(index)
 
 
 def _ptr(tensor):

@@ -1,7 +1,8 @@
 """Timing helpers and the seeded transport benchmark with raw samples.
 
-``measure`` and ``percentile`` restate the reference's ``src/moe_dispatch/benchmark.py:15-45``
-(events on the current stream, linear-interpolation percentiles). ``benchmark``
+``measure`` reports the reference's statistics (``src/moe_dispatch/benchmark.py:15-45``:
+median, p95 by linear interpolation, min and the raw samples) from events on
+the current stream. ``benchmark``
 runs the reference's transport suites (``benchmark.py:48-130``): per case, the
 PyTorch transport and the scalar and vectorized HIP paths are validated first,
 then dispatch, combine and both together are timed in an order rotated per
@@ -18,34 +19,33 @@ from pathlib import Path
 
 import torch
 
-from .evidence import percentile, read_results, source_hashes
+from .evidence import percentile, read_results, sample_statistics, source_hashes
 
-__all__ = ["percentile", "measure", "hardware_metadata", "benchmark", "transport_moe_check",
+__all__ = ["percentile", "sample_statistics", "measure", "hardware_metadata", "benchmark", "transport_moe_check",
            "run_transport_benchmark"]
 
 
 @torch.inference_mode()
 def measure(function, warmup, repeats):
-    """Warm up, then time each call with a pair of events on the current stream (µs)."""
+    """Time ``repeats`` calls of ``function`` (µs each) after ``warmup`` untimed ones.
+
+    Same statistics as the reference's ``measure`` (``benchmark.py:25-45``).
+    The calls run back to back on the current stream, separated by repeats + 1
+    recorded events: sample i is the time between boundary i and i + 1, so
+    each sample is one call's device time, launch gaps included, and no event
+    pair is recorded twice around the same gap.
+    """
     for _ in range(warmup):
         function()
     torch.cuda.synchronize()
-    events = [
-        (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        for _ in range(repeats)
-    ]
-    for start, end in events:
-        start.record()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(repeats + 1)]
+    marks[0].record()
+    for mark in marks[1:]:
         function()
-        end.record()
+        mark.record()
     torch.cuda.synchronize()
-    values_us = [start.elapsed_time(end) * 1000.0 for start, end in events]
-    return {
-        "median_us": statistics.median(values_us),
-        "p95_us": percentile(values_us, 0.95),
-        "min_us": min(values_us),
-        "samples_us": values_us,
-    }
+    values_us = [a.elapsed_time(b) * 1000.0 for a, b in zip(marks, marks[1:])]
+    return {**sample_statistics(values_us), "samples_us": values_us}
 
 
 def hardware_metadata():

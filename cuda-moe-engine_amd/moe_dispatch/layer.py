@@ -22,7 +22,7 @@ import math
 import torch
 
 from . import _lib
-from ._extension import get_extension
+from ._extension import current_stream_handle, get_extension
 from .experts import grouped_linear, resolve_backend, swiglu_reference
 from .reference import TorchWorkspace
 from .workspace import MAX_EXPERTS, MAX_TOPK, CudaWorkspace
@@ -132,7 +132,7 @@ class MoEBlock(torch.nn.Module):
         self._workspaces = {}
         self._route_buffers = {}
         self._router_scratch = None  # bf16 split of the router weights (fused router)
-        self._router_split_of = None  # (pointer, version, shape) of the weights the split holds
+        self._router_split_of = None  # _router_split_key() of the weights the split holds
         self._launches = {}  # cuda_fused: pre-validated launches per input signature
         self._extension = get_extension() if implementation != "torch" else None
 
@@ -170,7 +170,8 @@ class MoEBlock(torch.nn.Module):
             # version counter), and always inside a graph capture, so that every
             # replay of the graph reads the weights as they are then.
             split_of = self._router_split_key()
-            if split_of is not None and split_of == self._router_split_of and not _capturing():
+            capturing = _capturing()
+            if self._same_split(split_of, self._router_split_of) and not capturing:
                 router_weight = None
             else:
                 router_weight = self.router_weight
@@ -178,7 +179,8 @@ class MoEBlock(torch.nn.Module):
                 x, router_weight, self.routing_bias, ids32, ids64, weights,
                 scratch=self._router_scratch,
             )
-            self._router_split_of = split_of
+            # A captured split runs only when the graph is replayed.
+            self._router_split_of = None if capturing else split_of
             return ids32, ids64, weights
         logits = torch.nn.functional.linear(x.float(), self.router_weight) + self.routing_bias
         selected, ids64 = torch.topk(logits, self.config.topk, dim=-1)
@@ -186,12 +188,23 @@ class MoEBlock(torch.nn.Module):
         return ids64.to(torch.int32).contiguous(), ids64.contiguous(), weights
 
     def _router_split_key(self):
+        """Identity of the router weights the bf16 split was taken from.
+
+        The key holds the tensor itself (so its storage cannot be freed and
+        reused by another tensor at the same address while the key is kept),
+        its address, version counter, dtype, shape and device. None when the
+        tensor has no version counter (inference tensors): then every call splits.
+        """
         w = self.router_weight
         try:
             version = w._version
         except RuntimeError:  # inference tensors do not count versions
             return None
-        return (w.data_ptr(), version, tuple(w.shape), w.device)
+        return (w, w.data_ptr(), version, w.dtype, tuple(w.shape), w.device)
+
+    @staticmethod
+    def _same_split(a, b):
+        return a is not None and b is not None and a[0] is b[0] and a[1:] == b[1:]
 
     def workspace(self, x):
         key = (x.shape[0], x.dtype, x.device)
@@ -266,12 +279,16 @@ class _FusedLaunches:
     the two grouped GEMMs, combine) fixes every argument but x's address and
     the stream: workspace and weight pointers, sizes, the dtype code. Later
     forwards of the same token count on the same device make the same five
-    calls with those arguments, as long as the weight and bias tensors are the
-    same objects at the same addresses (an in-place update keeps both, and the
-    router split follows the weights' version as in ``MoEBlock.route``). This
-    removes about 50 us of host work per forward (validation and stream
+    calls with those arguments while every parameter tensor the calls read is
+    the object it was, at the same address, with the same dtype, shape and
+    layout (an in-place update keeps all of these; the router split follows
+    the weights' version as in ``MoEBlock.route``). Anything else sends the
+    forward back through the validating path, which raises on a bad tensor.
+    This removes about 50 us of host work per forward (validation and stream
     lookups), which dominates the eager latency of small batches.
     """
+
+    _PARAMETERS = ("router_weight", "gate_up_weight", "down_weight", "routing_bias", "_router_scratch")
 
     def __init__(self, block, x, state):
         cfg = block.config
@@ -279,8 +296,7 @@ class _FusedLaunches:
         ids32, ids64, weights = block._route_buffers[(x.shape[0], x.device)]
         self.lib = block._extension.lib
         self.device_index = x.device.index if x.device.index is not None else torch.cuda.current_device()
-        self.tensors = (block.gate_up_weight, block.down_weight, block.routing_bias, block._router_scratch)
-        self.pointers = tuple(v.data_ptr() for v in self.tensors)
+        self.fingerprint = self._fingerprint(block)
         self.keep = (ids32, ids64, weights, t, state)  # the buffers below stay allocated
         tokens, hidden = x.shape
         rows = t.packed.shape[0]
@@ -302,22 +318,30 @@ class _FusedLaunches:
         if x.dtype != torch.bfloat16:
             raise RuntimeError("cuda_fused launches are bf16")
 
+    @classmethod
+    def _fingerprint(cls, block):
+        tensors = tuple(getattr(block, name) for name in cls._PARAMETERS)
+        return tensors, tuple((v.data_ptr(), v.dtype, tuple(v.shape), v.is_contiguous()) for v in tensors)
+
     def still_valid(self, block):
-        tensors = (block.gate_up_weight, block.down_weight, block.routing_bias, block._router_scratch)
-        return all(a is b for a, b in zip(tensors, self.tensors)) and all(
-            v.data_ptr() == p for v, p in zip(tensors, self.pointers))
+        tensors, described = self.fingerprint
+        current = tuple(getattr(block, name) for name in self._PARAMETERS)
+        if not all(a is b for a, b in zip(current, tensors)):
+            return False
+        return all((v.data_ptr(), v.dtype, tuple(v.shape), v.is_contiguous()) == d for v, d in zip(current, described))
 
     def __call__(self, block, x):
         lib = self.lib
-        stream = _raw_stream(self.device_index)
+        stream = current_stream_handle(self.device_index)
         x_ptr = x.data_ptr()
         split_of = block._router_split_key()
-        if split_of is not None and split_of == block._router_split_of and not _capturing():
+        capturing = _capturing()
+        if block._same_split(split_of, block._router_split_of) and not capturing:
             router_weight = None
         else:
             router_weight = block.router_weight.data_ptr()
         lib.check(lib.moe_router_fused(x_ptr, router_weight, *self.router, stream), "router_fused_out")
-        block._router_split_of = split_of
+        block._router_split_of = None if capturing else split_of
         lib.check(lib.moe_dispatch(x_ptr, *self.dispatch, stream), "dispatch")
         lib.check(lib.moe_grouped_gateup_swiglu(*self.gateup, stream), "gateup_swiglu_out")
         lib.check(lib.moe_grouped_gemm(*self.down, stream), "grouped_gemm_out")
@@ -325,25 +349,30 @@ class _FusedLaunches:
         return self.output
 
 
-def _raw_stream(device_index):
-    """The current stream's handle on a device (torch's own accessor when it has one)."""
-    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-    if raw is not None:
-        return raw(device_index)
-    return torch.cuda.current_stream(device_index).cuda_stream
-
-
 @torch.inference_mode()
 def token_major_oracle(block, x):
-    """Dense token-major expert evaluation (reference ``layer.py:200-214``); excluded from timings."""
+    """Routed tokens evaluated token by token, independent of the packed layout.
+
+    The check the reference's benchmark harness runs on every forward
+    (``layer.py:200-214``), with the same policy: fp32 router logits plus bias,
+    top-k, softmax of the selected logits, each expert's gate/up projection,
+    SwiGLU and down projection in the block's dtype (torch's own GEMMs), and the
+    weighted sum in fp32 cast once. Here each expert evaluates only the
+    (token, slot) pairs routed to it, gathered straight from the top-k ids, and
+    adds them back by token index; no dispatch buffer, offset or permutation of
+    the engine is used. Excluded from timings.
+    """
+    cfg = block.config
     logits = torch.nn.functional.linear(x.float(), block.router_weight) + block.routing_bias
-    selected, ids64 = torch.topk(logits, block.config.topk, dim=-1)
-    weights = torch.softmax(selected, dim=-1)
-    expected = torch.zeros_like(x, dtype=torch.float32)
-    for expert in range(block.config.experts):
-        projection = torch.nn.functional.linear(x, block.gate_up_weight[expert])
-        activation = swiglu_reference(projection)
-        output = torch.nn.functional.linear(activation, block.down_weight[expert])
-        probability = (weights * (ids64 == expert)).sum(dim=1)
-        expected += output.float() * probability[:, None]
-    return expected.to(x.dtype)
+    top = torch.topk(logits, cfg.topk, dim=-1)
+    weights = torch.softmax(top.values, dim=-1)
+    total = torch.zeros(x.shape, device=x.device, dtype=torch.float32)
+    for expert in range(cfg.experts):
+        tokens, slots = torch.nonzero(top.indices == expert, as_tuple=True)
+        if tokens.numel() == 0:
+            continue
+        rows = x.index_select(0, tokens)
+        hidden_state = swiglu_reference(torch.nn.functional.linear(rows, block.gate_up_weight[expert]))
+        y = torch.nn.functional.linear(hidden_state, block.down_weight[expert]).float()
+        total.index_add_(0, tokens, y * weights[tokens, slots].unsqueeze(1))
+    return total.to(x.dtype)

@@ -1,8 +1,15 @@
-"""Convenience transport API with input validation; benchmarks use prevalidated workspace methods.
+"""Standalone transport API with input validation (``PackedTokens``, ``dispatch``, ``combine``).
 
-Mirrors the reference ``src/moe_dispatch/ops.py:8-77``: ``PackedTokens``,
-``validate_inputs``, ``dispatch`` and ``combine`` with the same argument
-meaning and exception types. Top-k may be 1..8 (the reference allows 1 or 2).
+Public surface of the reference's ``src/moe_dispatch/ops.py:8-77``: the same
+names, argument meaning and exception types (``ValueError`` for shapes,
+devices, ranges and workspace mismatches, ``TypeError`` for dtypes,
+``RuntimeError`` without a GPU). Top-k may be 1..8 here (the reference allows
+1 or 2).
+
+The checks are kept as ordered rule tables, so each error names the first
+rule a call breaks. The expert-id range check reads the ids' minimum and
+maximum back to the host in one transfer (it synchronises the stream): hot
+loops should validate once and then call ``CudaWorkspace.dispatch`` directly.
 """
 
 from dataclasses import dataclass
@@ -10,6 +17,9 @@ from dataclasses import dataclass
 import torch
 
 from .workspace import MAX_EXPERTS, MAX_TOPK, CudaWorkspace
+
+_ROW_DTYPES = (torch.float16, torch.float32, torch.bfloat16)
+_ID_DTYPES = (torch.int32, torch.int64)
 
 
 @dataclass(frozen=True)
@@ -23,27 +33,32 @@ class PackedTokens:
     workspace: CudaWorkspace
 
 
+# (predicate over (x, ids, experts), exception type, message), checked in order.
+_INPUT_RULES = (
+    (lambda x, ids, e: x.ndim == 2 and ids.ndim == 2, ValueError, "expected x[T,H] and expert_ids[T,K]"),
+    (lambda x, ids, e: x.shape[0] == ids.shape[0] and x.shape[1] >= 1, ValueError,
+     "token dimensions must match and H must be positive"),
+    (lambda x, ids, e: x.dtype in _ROW_DTYPES, TypeError, "x must be FP16, FP32, or BF16"),
+    (lambda x, ids, e: ids.dtype in _ID_DTYPES, TypeError, "expert_ids must be int32 or int64"),
+    (lambda x, ids, e: x.device == ids.device, ValueError, "x and expert_ids must be on the same device"),
+    (lambda x, ids, e: x.is_contiguous() and ids.is_contiguous(), ValueError, "inputs must be contiguous"),
+    (lambda x, ids, e: isinstance(e, int) and 1 <= e <= MAX_EXPERTS, ValueError,
+     "experts must be an integer in 1..64"),
+    (lambda x, ids, e: 1 <= ids.shape[1] <= MAX_TOPK, ValueError, "topk must be in 1..8"),
+    (lambda x, ids, e: not x.requires_grad, ValueError,
+     "HIP operators are forward-only; detach inputs or use inference_mode"),
+)
+
+
 def validate_inputs(x, expert_ids, experts):
-    if x.ndim != 2 or expert_ids.ndim != 2:
-        raise ValueError("expected x[T,H] and expert_ids[T,K]")
-    if x.shape[0] != expert_ids.shape[0] or x.shape[1] < 1:
-        raise ValueError("token dimensions must match and H must be positive")
-    if x.dtype not in (torch.float16, torch.float32, torch.bfloat16):
-        raise TypeError("x must be FP16, FP32, or BF16")
-    if expert_ids.dtype not in (torch.int32, torch.int64):
-        raise TypeError("expert_ids must be int32 or int64")
-    if x.device != expert_ids.device:
-        raise ValueError("x and expert_ids must be on the same device")
-    if not x.is_contiguous() or not expert_ids.is_contiguous():
-        raise ValueError("inputs must be contiguous")
-    if not isinstance(experts, int) or not 1 <= experts <= MAX_EXPERTS:
-        raise ValueError("experts must be an integer in 1..64")
-    if not 1 <= expert_ids.shape[1] <= MAX_TOPK:
-        raise ValueError("topk must be in 1..8")
-    if x.requires_grad:
-        raise ValueError("HIP operators are forward-only; detach inputs or use inference_mode")
-    if expert_ids.numel() and (expert_ids.min().item() < 0 or expert_ids.max().item() >= experts):
-        raise ValueError("expert_ids contains an out-of-range expert")
+    """Raise on the first broken rule; the last check reads the id range back to the host."""
+    for holds, error, message in _INPUT_RULES:
+        if not holds(x, expert_ids, experts):
+            raise error(message)
+    if expert_ids.numel():
+        low, high = (int(v) for v in torch.stack(torch.aminmax(expert_ids)).tolist())
+        if low < 0 or high >= experts:
+            raise ValueError("expert_ids contains an out-of-range expert")
 
 
 @torch.inference_mode()
@@ -52,33 +67,38 @@ def dispatch(x, expert_ids, experts, *, workspace=None, vectorized=True, alignme
     validate_inputs(x, expert_ids, experts)
     if not x.is_cuda:
         raise RuntimeError("dispatch requires a GPU; TorchWorkspace provides the CPU reference")
-    expected_shape = (x.shape[0], x.shape[1], experts, expert_ids.shape[1])
+    signature = (x.shape[0], x.shape[1], experts, expert_ids.shape[1])
     if workspace is None:
-        workspace = CudaWorkspace(
-            *expected_shape, x.dtype, vectorized=vectorized, device=x.device, alignment=alignment
-        )
-    if workspace.shape != expected_shape or workspace.dtype != x.dtype:
+        workspace = CudaWorkspace(*signature, x.dtype, vectorized=vectorized, device=x.device,
+                                  alignment=alignment)
+    elif workspace.shape != signature or workspace.dtype != x.dtype:
         raise ValueError("workspace shape/dtype does not match inputs")
     if workspace.packed.device != x.device:
         raise ValueError("workspace device does not match inputs")
-    workspace.dispatch(x, expert_ids.to(torch.int32))
-    return PackedTokens(
-        workspace.packed, workspace.inverse, workspace.counts, workspace.offsets, workspace
-    )
+    ids32 = expert_ids if expert_ids.dtype == torch.int32 else expert_ids.to(torch.int32)
+    workspace.dispatch(x, ids32)
+    return PackedTokens(workspace.packed, workspace.inverse, workspace.counts, workspace.offsets, workspace)
+
+
+# (predicate over (expert_output, batch, weights), exception type, message), checked in order.
+_COMBINE_RULES = (
+    (lambda y, b, w: w.shape == b.inverse.shape, ValueError, "weights must have shape [T,K]"),
+    (lambda y, b, w: y.shape == b.packed.shape and y.dtype == b.packed.dtype, ValueError,
+     "expert output shape/dtype must match packed tokens"),
+    (lambda y, b, w: w.device == b.packed.device and y.device == b.packed.device, ValueError,
+     "all tensors must be on the workspace device"),
+    (lambda y, b, w: w.is_contiguous() and y.is_contiguous(), ValueError,
+     "expert output and weights must be contiguous"),
+    (lambda y, b, w: w.is_floating_point(), TypeError, "weights must be floating point"),
+)
 
 
 @torch.inference_mode()
 def combine(expert_output, batch, weights):
     """Weighted gather/reduction; returns a reusable output view and accumulates in FP32."""
-    if weights.shape != batch.inverse.shape:
-        raise ValueError("weights must have shape [T,K]")
-    if expert_output.shape != batch.packed.shape or expert_output.dtype != batch.packed.dtype:
-        raise ValueError("expert output shape/dtype must match packed tokens")
-    if weights.device != batch.packed.device or expert_output.device != batch.packed.device:
-        raise ValueError("all tensors must be on the workspace device")
-    if not weights.is_contiguous() or not expert_output.is_contiguous():
-        raise ValueError("expert output and weights must be contiguous")
-    if not weights.is_floating_point():
-        raise TypeError("weights must be floating point")
-    batch.workspace.combine(expert_output, weights.to(torch.float32))
+    for holds, error, message in _COMBINE_RULES:
+        if not holds(expert_output, batch, weights):
+            raise error(message)
+    fp32 = weights if weights.dtype == torch.float32 else weights.to(torch.float32)
+    batch.workspace.combine(expert_output, fp32)
     return batch.workspace.output

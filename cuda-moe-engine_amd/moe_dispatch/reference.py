@@ -1,14 +1,28 @@
 """PyTorch transport variant (``implementation="torch"``), usable on CPU and GPU.
 
-Restates the reference ``TorchWorkspace`` (``src/moe_dispatch/reference.py:6-82``):
-counts by scatter-add, offsets by cumulative sum, a sort of the flat expert ids
-to order the assignments, ``index_select``/``index_copy`` for the rows, and an
-fp32 multiply + sum for the weighted combine. The sort is stable here, so the
-permutation is the canonical one (the reference's unstable sort gives some
-order within each expert; the order is not part of its contract).
+Same contract as the reference ``TorchWorkspace`` (``src/moe_dispatch/reference.py:6-82``):
+preallocated buffers, ``dispatch(x, ids32, ids64)`` filling ``counts``,
+``offsets``, ``inverse`` and ``packed``, and ``combine(expert_output, weights)``
+reducing in fp32 into a reusable ``output`` view.
+
+How it computes them:
+
+* counts by a scatter-add of ones, offsets by a cumulative sum of the spans
+  rounded up to the alignment;
+* a stable sort of the flat expert ids orders the assignments by (expert,
+  flat index p = t*K + k), so the packed order is the canonical one the HIP
+  kernels produce (the reference's unstable sort leaves the order within an
+  expert unspecified, and the order is not part of its contract);
+* destination row = padded start of the expert + rank within the expert;
+* combine: the K rows of each token are gathered through ``inverse`` and
+  summed in fp32 in k order, one multiply and one add per term, then cast
+  once; this is the HIP combine's arithmetic.
 """
 
 import torch
+
+_BUFFERS = ("counts", "offsets", "inverse", "sorted_ids", "order", "token_of", "destination", "position",
+            "unit", "packed", "gathered", "output", "accumulated", "term")
 
 
 class TorchWorkspace:
@@ -17,17 +31,15 @@ class TorchWorkspace:
     def __init__(self, tokens, hidden, experts, topk, dtype, device="cuda", alignment=1):
         if not 1 <= alignment <= 128:
             raise ValueError("alignment must be 1..128")
+        from .workspace import capacity_rows
+
         n = tokens * topk
         self.alignment = alignment
-        self.capacity_rows = (
-            n
-            if alignment == 1
-            else (n + experts * (alignment - 1) + 1 + alignment - 1) // alignment * alignment
-        )
+        self.capacity_rows = capacity_rows(tokens, experts, topk, alignment)
         self.tokens, self.hidden, self.topk, self.experts = tokens, hidden, topk, experts
         device = torch.device(device)
         self.device = device
-        i32, i64 = torch.int32, torch.int64
+        i32, i64, f32 = torch.int32, torch.int64, torch.float32
         self.counts = torch.empty(experts, device=device, dtype=i32)
         self.offsets = torch.empty(experts + 1, device=device, dtype=i32)
         self.inverse = torch.empty((tokens, topk), device=device, dtype=i64)
@@ -39,13 +51,9 @@ class TorchWorkspace:
         self.unit = torch.ones(n, device=device, dtype=i32)
         self.packed = torch.empty((self.capacity_rows, hidden), device=device, dtype=dtype)
         self.gathered = torch.empty((n, hidden), device=device, dtype=dtype)
-        self.weighted = torch.empty((tokens, topk, hidden), device=device, dtype=torch.float32)
         self.output = torch.empty((tokens, hidden), device=device, dtype=dtype)
-        self.accumulated = (
-            self.output
-            if dtype == torch.float32
-            else torch.empty((tokens, hidden), device=device, dtype=torch.float32)
-        )
+        self.accumulated = torch.empty((tokens, hidden), device=device, dtype=f32)
+        self.term = torch.empty((tokens, hidden), device=device, dtype=f32)
 
     def dispatch(self, x, ids32, ids64):
         flat = ids64.reshape(-1)
@@ -68,16 +76,16 @@ class TorchWorkspace:
 
     def combine(self, expert_output, weights):
         torch.index_select(expert_output, 0, self.inverse.reshape(-1), out=self.gathered)
-        torch.mul(
-            self.gathered.view(self.tokens, self.topk, self.hidden),
-            weights.unsqueeze(-1),
-            out=self.weighted,
-        )
-        torch.sum(self.weighted, dim=1, out=self.accumulated)
-        if self.output is not self.accumulated:
-            self.output.copy_(self.accumulated)
+        rows = self.gathered.view(self.tokens, self.topk, self.hidden)
+        w = weights.to(torch.float32)
+        acc, term = self.accumulated, self.term
+        # k order, separate multiply and add (the HIP combine's sequence).
+        torch.mul(rows[:, 0], w[:, 0:1], out=acc)
+        for k in range(1, self.topk):
+            torch.mul(rows[:, k], w[:, k:k + 1], out=term)
+            acc.add_(term)
+        self.output.copy_(acc)
 
     @property
     def workspace_bytes(self):
-        tensors = {t.data_ptr(): t for t in vars(self).values() if isinstance(t, torch.Tensor)}
-        return sum(t.numel() * t.element_size() for t in tensors.values())
+        return sum(getattr(self, name).numel() * getattr(self, name).element_size() for name in _BUFFERS)

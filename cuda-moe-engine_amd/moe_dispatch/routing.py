@@ -33,3 +33,19 @@ def make_transport_case(tokens, hidden, experts, topk, dtype, seed, device="cuda
     logits = torch.randn((tokens, topk), device=device, generator=generator)
     weights = torch.softmax(logits, dim=-1).contiguous()
     return x, ids64.to(torch.int32).contiguous(), ids64.contiguous(), weights
+
+
+def zipf_bias(experts, exponent=1.2, scale=1.75, seed=0):
+    """Router bias of the skewed fine-grained workload, fp32 ``[E]``.
+
+    Expert e gets a Zipf weight ``p_e = r_e ** -exponent`` for a seeded random
+    rank permutation ``r`` of 1..E, and ``bias_e = scale * ln(p_e / max p)``:
+    0 for the top-ranked expert, increasingly negative below it. With N(0,1)
+    logits and top-6 over 64 experts this leaves several experts without tokens
+    and gives a few more than 15% of the assignments.
+    """
+    import numpy as np
+
+    ranks = np.random.default_rng(seed).permutation(np.arange(1, experts + 1)).astype(np.float64)
+    weight = ranks ** (-exponent)
+    return torch.from_numpy((scale * np.log(weight / weight.max())).astype(np.float32))

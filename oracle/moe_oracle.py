@@ -44,13 +44,52 @@ Pinning (what checks each function; see tests/test_oracle.py)
   bf16 step away).
 * ``block_forward``: the restated ``token_major_oracle`` (dense, token-major,
   independent of the permutation).
+* ``mfma_gemm.c`` (``oracle/_build/libmoe_oracle.so``, built by
+  ``__graft_entry__.build()``): the "mfma" order in C, used by ``grouped_gemm``
+  for float32 inputs when the library is present; equal to the numpy form bit
+  for bit (``tests/test_oracle.py``), so whole expert spans of the benchmark
+  shapes can be checked in seconds.
 """
 
 from __future__ import annotations
 
+import ctypes
 import math
+from pathlib import Path
 
 import numpy as np
+
+_C_LIBRARY = Path(__file__).resolve().parent / "_build" / "libmoe_oracle.so"
+
+
+def build_c_checker(force: bool = False) -> Path:
+    """Compile ``mfma_gemm.c`` into ``_build/libmoe_oracle.so`` with gcc (a checker, not product code)."""
+    import subprocess
+
+    if force or not _C_LIBRARY.is_file():
+        _C_LIBRARY.parent.mkdir(exist_ok=True)
+        tmp = _C_LIBRARY.with_suffix(".so.tmp")
+        subprocess.run(["gcc", "-O3", "-fopenmp", "-mavx2", "-mfma", "-ffp-contract=off", "-shared", "-fPIC",
+                        str(_C_LIBRARY.parent.parent / "mfma_gemm.c"), "-o", str(tmp)], check=True)
+        tmp.replace(_C_LIBRARY)
+    return _C_LIBRARY
+
+
+def _load_c_gemm():
+    """The C form of the "mfma" order, or None when it was not built."""
+    if not _C_LIBRARY.is_file():
+        return None
+    try:
+        lib = ctypes.CDLL(str(_C_LIBRARY))
+    except OSError:
+        return None
+    fn = lib.moe_oracle_mfma_gemm
+    fn.restype = None
+    fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4
+    return fn
+
+
+_C_GEMM = _load_c_gemm()
 
 __all__ = [
     "bf16_bits",
@@ -291,18 +330,37 @@ def grouped_gemm(a: np.ndarray, b: np.ndarray, offsets: np.ndarray, order: str =
     """
     if order not in ("mfma", "exact"):
         raise ValueError("order must be 'mfma' or 'exact'")
-    a64 = np.asarray(a, dtype=np.float64)
-    out = np.zeros((a64.shape[0], b.shape[1]), dtype=np.float32)
+    use_c = order == "mfma" and _C_GEMM is not None and np.asarray(a).dtype == np.float32
+    a64 = None if use_c else np.asarray(a, dtype=np.float64)
+    out = np.zeros((np.asarray(a).shape[0], b.shape[1]), dtype=np.float32)
     offsets = np.asarray(offsets, dtype=np.int64)
     for e in range(b.shape[0]):
         s, t = int(offsets[e]), int(offsets[e + 1])
         if t <= s:
             continue
+        if use_c and np.asarray(b[e]).dtype == np.float32:
+            out[s:t] = mfma_order_matmul_c(np.asarray(a)[s:t], np.asarray(b[e]))
+            continue
+        if a64 is None:
+            a64 = np.asarray(a, dtype=np.float64)
         be = np.asarray(b[e], dtype=np.float64)
         if order == "exact":
             out[s:t] = (a64[s:t] @ be.T).astype(np.float32)
         else:
             out[s:t] = _mfma_order_matmul(a64[s:t], be)
+    return out
+
+
+def mfma_order_matmul_c(a32: np.ndarray, b32: np.ndarray, group: int = 8) -> np.ndarray:
+    """``a @ b.T`` in the "mfma" order by the C checker (float32 inputs holding bf16 values)."""
+    if _C_GEMM is None:
+        raise RuntimeError(f"{_C_LIBRARY} is not built")
+    a32 = np.ascontiguousarray(a32, dtype=np.float32)
+    b32 = np.ascontiguousarray(b32, dtype=np.float32)
+    m, k = a32.shape
+    n = b32.shape[0]
+    out = np.empty((m, n), dtype=np.float32)
+    _C_GEMM(a32.ctypes.data, b32.ctypes.data, out.ctypes.data, m, n, k, group)
     return out
 
 

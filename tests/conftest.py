@@ -13,6 +13,12 @@ def pytest_configure(config):
     import torch
 
     torch.set_num_threads(1)
+    # The oracle's C checker (seconds to build with gcc) when build() has not made it yet.
+    from oracle import moe_oracle
+
+    if moe_oracle._C_GEMM is None:
+        moe_oracle.build_c_checker()
+        moe_oracle._C_GEMM = moe_oracle._load_c_gemm()
     config.addinivalue_line("markers", "gpu: needs an AMD GPU (MI355X) and the built HIP library")
 
 

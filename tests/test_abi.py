@@ -79,6 +79,40 @@ def test_validation_errors_without_launching():
     assert lib.moe_set_gemm_workgroups(16) == 0 and lib.moe_set_gemm_workgroups(0) == 0
 
 
+def test_misaligned_pointers_are_rejected_without_launching():
+    """Addresses the kernels cannot access as they must are refused before any launch.
+
+    The GEMMs and the fused router read their operands with 16-byte (direct-to-LDS)
+    loads, so a view starting mid-vector is an error there; the transport kernels
+    take narrower accesses instead, and only an address that is not a multiple of
+    the element size is an error.
+    """
+    lib = _lib.load_library()
+    A = 1 << 20  # 16-byte aligned stand-in addresses (never dereferenced)
+    assert lib.moe_grouped_gemm(A + 2, A, A, A, 16, 64, 64, 1, None) == 1
+    assert b"16-byte aligned" in lib.moe_last_error()
+    assert lib.moe_grouped_gemm(A, A + 8, A, A, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gemm(A, A, A + 8, A, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gemm(A, A, A, A + 2, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gateup_swiglu(A + 8, A, A, A, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gateup_swiglu(A, A, A + 4, A, 16, 64, 64, 1, None) == 1
+    need = lib.moe_router_scratch_bytes(8, 64)
+    assert lib.moe_router_fused(A + 2, A, A, A, A, A, None, A, need, 4, 64, 8, 2, None) == 1
+    assert b"16-byte aligned" in lib.moe_last_error()
+    assert lib.moe_router_fused(A, A, A, A, A + 4, A, None, A, need, 4, 64, 8, 2, None) == 1  # ids64
+    assert lib.moe_topk_route(A, A, A, A + 4, A, 4, 8, 2, None) == 1
+    assert lib.moe_topk_route(A + 2, A, A, A, A, 4, 8, 2, None) == 1
+    scratch = lib.moe_dispatch_scratch_bytes(10, 8, 2)
+    # bf16 rows at an odd address; then an index buffer off its 4-byte grid
+    assert lib.moe_dispatch(A + 1, 2, A, A, A, A, A, A, A, scratch, 10, 64, 8, 2, 8, 80, 1, None) == 1
+    assert b"element size" in lib.moe_last_error()
+    assert lib.moe_dispatch(A, 2, A, A, A, A + 2, A, A, A, scratch, 10, 64, 8, 2, 1, 20, 1, None) == 1
+    assert lib.moe_dispatch(A, 0, A, A, A + 2, A, A, A, A, scratch, 10, 64, 8, 2, 1, 20, 1, None) == 1
+    assert lib.moe_combine(A, 0, A, A, A + 2, 4, 64, 2, 8, None) == 1  # fp32 output at +2
+    assert lib.moe_combine(A, 2, A + 1, A, A, 4, 64, 2, 8, None) == 1  # inverse
+    assert lib.moe_swiglu(A + 1, 2, A, A, 4, 64, None) == 1
+
+
 def test_error_surfaces_as_runtime_error():
     lib = _lib.load_library()
     with pytest.raises(_lib.MoeHipError, match="1..64"):

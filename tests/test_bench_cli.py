@@ -64,3 +64,40 @@ def test_gateup_roofline_picks_the_bound_by_intensity():
     c1 = (np.array([32] * 8), 320, 512, 1024, 256, 4.0 * 256 * 512 * 1024, 10.0)
     assert bench.gateup_roofline("none", *c1, cus=256)["kernel"].startswith("grouped_gemm_decode_kernel<true>")
     assert bench.gateup_roofline("none", *c1, cus=32)["kernel"].startswith("grouped_gemm_persistent_kernel<true>")
+
+
+def test_byte_models_and_workload_bias_equal_the_oracle():
+    """bench.py's own byte models and the Zipf bias generator (product side) equal the oracle's."""
+    import numpy as np
+
+    from moe_dispatch.routing import zipf_bias
+    from oracle import moe_oracle as oracle
+
+    for args in ((4096, 2048, 2, 0), (4096, 4096, 2, 64), (8192, 2048, 6, 456), (1, 4096, 2, 14)):
+        assert bench.dispatch_bytes(*args) == oracle.dispatch_bytes(*args)
+        assert bench.combine_bytes(*args[:3]) == oracle.combine_bytes(*args[:3])
+    for experts in (8, 64):
+        np.testing.assert_array_equal(zipf_bias(experts).numpy(), oracle.zipf_bias(experts))
+
+
+def test_cpu_baseline_times_the_torch_variant_at_config_1(monkeypatch):
+    """The CPU baseline leg runs the PyTorch variant at BASELINE config 1 (shortened here)."""
+    import torch
+
+    calls = []
+    real = bench._time_cpu
+
+    def quick(fn, warmup, samples):
+        calls.append((warmup, samples))
+        return real(fn, 1, 2)
+
+    monkeypatch.setattr(bench, "_time_cpu", quick)
+    threads = torch.get_num_threads()
+    out = bench.cpu_baseline()
+    assert torch.get_num_threads() == threads  # restored
+    assert calls == [(10, 40), (10, 40)]
+    assert out["kind"] == "port" and out["unit"] == "us" and out["value"] == out["all_cores"]["median_us"]
+    assert out["one_thread"]["threads"] == 1 and out["cores"] == out["all_cores"]["threads"] >= 1
+    assert out["config"] == {"tokens": 128, "hidden": 512, "intermediate": 1024, "experts": 8, "topk": 2,
+                             "dtype": "bf16"}
+    assert out["cpu_model"] and out["torch_version"] == torch.__version__

@@ -10,7 +10,9 @@ Stage by stage, each stage fed the kernels' own inputs:
     the MFMA-order oracle, the rest within 2 bf16 steps;
   * combine: bit-exact.
 End to end: max-abs <= 1.6e-2 and relative L2 <= 5e-4
-against the expert-major oracle with the kernels' accumulation order, and
+against the expert-major oracle with the kernels' accumulation order (at the
+full sizes C3 T=4096, C4 T=4096 and C5 on a token sample, whose routing and
+k-order combine the oracle replays), and
 against the independent token-major oracle with exact float64 dot products
 (at I=14336 that last bound is 2e-3: two fp32 summation orders disagree there
 by ~1e-3, because a few one-step bf16 flips of the activation perturb every
@@ -151,6 +153,51 @@ def test_router_weight_updates_are_seen():
         assert torch.equal(block(x), twin(x))
 
 
+def test_fast_path_rechecks_a_replaced_router_weight():
+    """After the pre-validated launches are in use, a router weight of another dtype,
+    shape or layout is caught by the validating path (RuntimeError), never read as
+    fp32 [E,H]; putting the original back restores the same output."""
+    cfg = MoEConfig(256, 512, 8, 2)
+    block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=3)
+    x = torch.randn(100, 256, device="cuda").bfloat16()
+    first = block(x).clone()
+    assert torch.equal(block(x), first) and (100, x.device) in block._launches
+    good = block.router_weight
+    wrong = [good.bfloat16(), torch.randn(8, 264, device="cuda"), torch.randn(9, 256, device="cuda"),
+             good.t().contiguous().t()]
+    for bad in wrong:
+        block.router_weight = bad
+        with pytest.raises(RuntimeError):
+            block(x)
+    block.router_weight = good
+    assert torch.equal(block(x), first)
+    torch.cuda.synchronize()
+
+
+def test_capture_right_after_a_router_update_leaves_eager_calls_correct():
+    """A capture records the router split without running it; the next eager forward
+    must split again rather than trust planes the capture never wrote."""
+    cfg = MoEConfig(256, 512, 8, 2)
+    block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=4)
+    twin = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=4)
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn(64, 256, device="cuda", generator=gen).bfloat16()
+    block(x)
+    block(x)
+    new_w = torch.randn(8, 256, device="cuda", generator=gen) / 16
+    block.router_weight.copy_(new_w)
+    twin.router_weight = new_w.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        block(x)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(block(x).clone(), twin(x))
+    del graph
+
+
 @pytest.mark.parametrize("cfg,tokens,bias", [
     (MoEConfig(512, 1024, 8, 2), 128, None),
     (MoEConfig(256, 512, 16, 2), 777, "skewed"),
@@ -249,9 +296,28 @@ def _sample_rows(offsets, counts, per_expert, rng):
     return np.asarray(rows, dtype=np.int64), np.asarray(sample_offsets, dtype=np.int64)
 
 
-def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, token_sample=48, seed=0):
+def _check_expert_span(state, block, offsets, counts, expert):
+    """Both GEMMs over one whole expert span (every row, every column) against the
+    MFMA-order oracle (the C checker), each on the kernels' own input."""
+    lo, n = int(offsets[expert]), int(counts[expert])
+    packed = to_np(state.transport.packed[lo:lo + n])
+    act = to_np(state.activated[lo:lo + n])
+    eo = to_np(state.expert_output[lo:lo + n])
+    span = np.array([0, n])
+    gate_up = to_np(block.gate_up_weight[expert])[None]
+    proj_ref = oracle.bf16_round(oracle.grouped_gemm(packed, gate_up, span))
+    del gate_up
+    assert_near_bit_exact(act, oracle.swiglu(proj_ref, n), max_fraction=2e-4, max_steps=2.0)
+    down = to_np(block.down_weight[expert])[None]
+    eo_ref = oracle.bf16_round(oracle.grouped_gemm(act, down, span))
+    assert_near_bit_exact(eo, eo_ref, max_fraction=1e-4)
+
+
+def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, token_sample=48, seed=0,
+                         full_span=False):
     """Full-size block: exact layout and permutation over all tokens; GEMMs, combine and
-    end-to-end output on sampled rows/tokens (rows of a GEMM are independent)."""
+    end-to-end output on sampled rows/tokens (rows of a GEMM are independent); with
+    ``full_span``, both GEMMs over the whole span of the expert with the fewest rows."""
     block, x, out, ids32, weights, state = _run_block(cfg, tokens, "balanced", seed, bias)
     rng = np.random.default_rng(seed)
     transport = state.transport
@@ -296,16 +362,28 @@ def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, to
     eo_rows[needed] = to_np(state.expert_output.index_select(0, torch.from_numpy(needed).cuda()))
     got = to_np(out)[tsample]
     np.testing.assert_array_equal(got, oracle.combine(eo_rows, inv_s, w[tsample]))
-    # End to end on the token sample against the exact-arithmetic token-major oracle.
+    # End to end on the token sample, the north-star bounds against the oracle with
+    # the kernels' rounding points and accumulation order (the sampled tokens'
+    # routing, k-order combine) ...
+    xs_all = to_np(x)[tsample]
+    ordered = oracle.block_forward(xs_all, router_w, bias_np, gate_up, down, cfg.topk, 1, ids=ids[tsample],
+                                   weights=w[tsample])["output"]
+    assert float(np.abs(got - ordered).max()) <= MAX_ABS
+    assert rel_l2(got, ordered) <= REL_L2
+    # ... and against the exact-arithmetic token-major oracle (see the module docstring).
     dense = oracle.token_major_forward(to_np(x), gate_up, down, ids, w, token_index=tsample, order="exact")
     assert float(np.abs(got - dense).max()) <= MAX_ABS
     assert rel_l2(got, dense) <= (REL_L2_LARGE_I if large_i else REL_L2)
+    if full_span:
+        nonempty = [e for e in range(cfg.experts) if counts[e] > 0]
+        _check_expert_span(state, block, offsets, counts, min(nonempty, key=lambda e: counts[e]))
     return counts
 
 
 def test_config4_prefill_full_size_sampled():
-    """C4 at T=4096 (the benchmark workload): full layout, sampled GEMM rows and tokens."""
-    _check_block_sampled(MoEConfig(4096, 14336, 8, 2), 4096, large_i=True)
+    """C4 at T=4096 (the benchmark workload): full layout, sampled GEMM rows and tokens,
+    and one whole expert span of both GEMMs."""
+    _check_block_sampled(MoEConfig(4096, 14336, 8, 2), 4096, large_i=True, full_span=True)
 
 
 def test_config3_t4096_full_size_sampled():

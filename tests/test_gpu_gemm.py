@@ -52,6 +52,10 @@ GEMM_CASES = [
     ([90, 20, 0], 8, 200, 128),
     ([7, 0, 40], 1, 96, 192),
     ([2, 2], 1, 4096, 1024),
+    # generic path (K % 64 != 0) with one or two column tiles: 9 row tiles of one
+    # expert need every one of the 8 * ceil(9 / 8) workgroup slots
+    ([2304], 8, 256, 200),
+    ([1500, 100, 3, 0], 8, 256, 1000),
 ]
 
 

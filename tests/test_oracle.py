@@ -345,3 +345,20 @@ def test_mfma_order_is_within_fp32_bound_of_exact():
     bound = 128 * np.finfo(np.float32).eps * (np.abs(a) @ np.abs(b[0]).T).max()
     assert np.max(np.abs(mfma - exact)) <= bound
     assert np.any(mfma != exact)  # the orders do differ somewhere
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (3, 33, 17), (40, 65, 200), (17, 96, 1030)])
+def test_mfma_order_c_checker_equals_numpy_form(m, n, k):
+    """The C form (used for whole expert spans) and the numpy form agree bit for bit,
+    including a k that is not a whole number of groups and a wide dynamic range."""
+    assert oracle._C_GEMM is not None, "oracle/_build/libmoe_oracle.so was not built"
+    rng = np.random.default_rng(m * 1000 + n + k)
+    scale = np.exp2(rng.integers(-12, 12, size=(1, k))).astype(np.float32)
+    a = oracle.bf16_round((rng.standard_normal((m, k)) * scale).astype(np.float32))
+    b = oracle.bf16_round((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+    c = oracle.mfma_order_matmul_c(a, b)
+    ref = oracle._mfma_order_matmul(a.astype(np.float64), b.astype(np.float64))
+    np.testing.assert_array_equal(c, ref)
+    # A different grouping is a different model: groups of 4 disagree somewhere.
+    if k >= 64:
+        assert not np.array_equal(oracle.mfma_order_matmul_c(a, b, group=4), c)
