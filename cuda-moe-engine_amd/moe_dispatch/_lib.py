@@ -36,6 +36,10 @@ _SIGNATURES = {
         _int,
         [_c_void_p, _int] + [_c_void_p] * 7 + [_i64] * 7 + [_int, _c_void_p],
     ),
+    "moe_dispatch_noalloc": (
+        _int,
+        [_c_void_p, _int] + [_c_void_p] * 6 + [_i64] * 6 + [_int, _c_void_p],
+    ),
     "moe_combine": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 4 + [_c_void_p]),
     "moe_swiglu": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "moe_grouped_gemm": (_int, [_c_void_p] * 4 + [_i64] * 4 + [_c_void_p]),

@@ -123,6 +123,23 @@ int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, 
                  void* stream);
 
 /*
+ * moe_dispatch with no scratch argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. It allocates
+ * nothing: the kernels' per-chunk count table (at most 4096 bytes for every
+ * valid shape; larger needs return MOE_ERR_WORKSPACE) lives in a static device
+ * array of the library, one per GPU, kept until the process ends. Every call
+ * on one GPU uses that GPU's array, so calls that overlap in time on one GPU
+ * (other streams or host threads) race; calls on one stream are ordered. The
+ * current device must be the one the pointers and the stream belong to.
+ * Arguments, results and errors are otherwise moe_dispatch's.
+ */
+int moe_dispatch_noalloc(const void* x, int dtype, const int32_t* ids, int32_t* counts,
+                         int32_t* offsets, int32_t* slots, void* packed, int32_t* inverse,
+                         int64_t tokens, int64_t hidden, int64_t experts, int64_t topk,
+                         int64_t alignment, int64_t packed_rows, int vectorized, void* stream);
+
+/*
  * Weighted combine: out[t] = round(sum_k w[t,k] * float(y[inverse[t,k]])),
  * fp32 products and running sum in k order (no fused multiply-add), rows
  * outside [0, packed_rows) skipped, no atomics.
