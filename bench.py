@@ -74,6 +74,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch-variant", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replay timing")
+    ap.add_argument("--gemm-study", action="store_true",
+                    help="time the expert GEMMs beside hipBLASLt, a dense one-expert problem and zero weights")
     ap.add_argument("--cpu-sample-tokens", type=int, default=64,
                     help="tokens of the benchmark workload the CPU variant also runs (0: config 1 only)")
     return ap.parse_args(argv)
@@ -391,6 +393,72 @@ def transport_bench(args):
     return 0
 
 
+def gemm_study(block, x, args):
+    """Expert GEMMs beside hipBLASLt and the same kernels on a dense problem (one JSON line).
+
+    For the configuration's real routing: the gate/up (+ SwiGLU) and down grouped
+    GEMMs; torch.matmul (hipBLASLt) on dense bf16 GEMMs of the same total shape
+    (M = assignments); this build's kernels on one expert holding all M rows (no
+    short row tiles); and the grouped GEMMs again with zero weights, which keeps
+    the schedule and the data movement but not the multiplier activity. Run it
+    under rocprofv3 --pmc to read the clock (GRBM_GUI_ACTIVE) and MFMA busy
+    cycles of each launch; the kernels run in the order listed.
+    """
+    import torch
+
+    cfg = block.config
+    state = block.workspace(x)
+    t = state.transport
+    ext = block._extension
+    n = x.shape[0] * cfg.topk
+    h, i = cfg.hidden, cfg.intermediate
+    steps, warm = args.steps, max(args.warmup, 3)
+    flop_gu, flop_dn = 4.0 * n * h * i, 2.0 * n * h * i
+    rows = {}
+
+    def row(name, fn, flop):
+        us = time_loop(fn, steps, warm)
+        rows[name] = {"us": round(us, 2), "tflops": round(flop / (us * 1e-6) / 1e12, 1),
+                      "mfma_frac": round(flop / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+    with torch.inference_mode():
+        block(x)
+        row("gateup_swiglu", lambda: ext.gateup_swiglu_out(t.packed, block.gate_up_weight, t.offsets,
+                                                           state.activated), flop_gu)
+        row("down", lambda: ext.grouped_gemm_out(state.activated, block.down_weight, t.offsets,
+                                                 state.expert_output), flop_dn)
+        gen = torch.Generator(device=x.device).manual_seed(3)
+        a = torch.randn(n, h, device=x.device, generator=gen).bfloat16()
+        b = torch.randn(2 * i, h, device=x.device, generator=gen).bfloat16()
+        row("hipblaslt_gateup_shape", lambda: torch.matmul(a, b.t()), flop_gu)
+        del b
+        a2 = torch.randn(n, i, device=x.device, generator=gen).bfloat16()
+        b2 = torch.randn(h, i, device=x.device, generator=gen).bfloat16()
+        row("hipblaslt_down_shape", lambda: torch.matmul(a2, b2.t()), flop_dn)
+        del a2, b2
+        one = torch.tensor([0, n], device=x.device, dtype=torch.int32)
+        act = torch.empty(n, i, device=x.device, dtype=torch.bfloat16)
+        out = torch.empty(n, h, device=x.device, dtype=torch.bfloat16)
+        gu1 = block.gate_up_weight[:1]
+        dn1 = block.down_weight[:1]
+        row("gateup_swiglu_one_expert", lambda: ext.gateup_swiglu_out(a, gu1, one, act), flop_gu)
+        row("down_one_expert", lambda: ext.grouped_gemm_out(act, dn1, one, out), flop_dn)
+        del a, act, out
+        zero_gu = torch.zeros_like(block.gate_up_weight)
+        row("gateup_swiglu_zero_weights", lambda: ext.gateup_swiglu_out(t.packed, zero_gu, t.offsets,
+                                                                        state.activated), flop_gu)
+        del zero_gu
+        zero_dn = torch.zeros_like(block.down_weight)
+        row("down_zero_weights", lambda: ext.grouped_gemm_out(state.activated, zero_dn, t.offsets,
+                                                              state.expert_output), flop_dn)
+        del zero_dn
+    torch.cuda.synchronize()
+    print(json.dumps({"gemm_study": args.config, "assignments": n, "hidden": h, "intermediate": i,
+                      "experts": cfg.experts, "expert_counts": t.counts.tolist(), "steps": steps,
+                      "warmup": warm, "rows": rows}), flush=True)
+    return 0
+
+
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
@@ -417,6 +485,8 @@ def main(argv=None):
         block.set_routing_bias(zipf_bias(experts))
     gen = torch.Generator(device=device).manual_seed(0)
     x = torch.randn(tokens, hidden, device=device, generator=gen).bfloat16()
+    if args.gemm_study:
+        return gemm_study(block, x, args)
 
     with torch.inference_mode():
         for _ in range(args.warmup):

@@ -14,6 +14,7 @@ int launch_topk_route(const float*, const float*, int32_t*, int64_t*, float*, in
                       hipStream_t);
 int launch_router_fused(const uint16_t*, const float*, const float*, int32_t*, int64_t*, float*,
                         float*, uint16_t*, int64_t, int, int, int, hipStream_t);
+int launch_router_split(const float*, uint16_t*, int, int, hipStream_t);
 int64_t router_scratch_bytes(int64_t, int64_t);
 int64_t dispatch_scratch_bytes(int64_t, int64_t, int64_t);
 int launch_dispatch(const void*, int, const int32_t*, int32_t*, int32_t*, int32_t*, void*,
@@ -136,6 +137,21 @@ int moe_router_fused(const void* x, const float* router_w, const float* bias, in
     return launch_router_fused(static_cast<const uint16_t*>(x), router_w, bias, ids32, ids64,
                                weights, logits_out, static_cast<uint16_t*>(scratch), tokens,
                                (int)hidden, (int)experts, (int)topk, static_cast<hipStream_t>(stream));
+}
+
+int moe_router_split(const float* router_w, void* scratch, int64_t scratch_bytes, int64_t experts,
+                     int64_t hidden, void* stream) {
+    MOE_REQUIRE(hidden >= 8 && hidden % 8 == 0 && hidden <= (1 << 20), MOE_ERR_UNSUPPORTED,
+                "fused router needs hidden a positive multiple of 8 up to 1048576");
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "routing supports 1..64 experts");
+    const int64_t need = router_scratch_bytes(experts, hidden);
+    MOE_REQUIRE(router_w && scratch, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(scratch_bytes >= need, MOE_ERR_WORKSPACE, "router scratch needs %lld bytes, got %lld",
+                (long long)need, (long long)scratch_bytes);
+    MOE_REQUIRE(aligned_to(router_w, 16) && aligned_to(scratch, 16), MOE_ERR_INVALID_ARGUMENT,
+                "router weights and scratch must be 16-byte aligned");
+    return launch_router_split(router_w, static_cast<uint16_t*>(scratch), (int)experts, (int)hidden,
+                               static_cast<hipStream_t>(stream));
 }
 
 int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {

@@ -525,16 +525,20 @@ int64_t router_scratch_bytes(int64_t experts, int64_t hidden) {
     return router_partials_offset(experts, hidden) + kRouterPartialBytes;
 }
 
+int launch_router_split(const float* router_w, uint16_t* planes, int experts, int hidden, hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(experts) * hidden;
+    hipLaunchKernelGGL(router_split_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0, stream,
+                       router_w, planes, n);
+    return check_launch("router_split_kernel");
+}
+
 int launch_router_fused(const uint16_t* x, const float* router_w, const float* bias,
                         int32_t* ids32, int64_t* ids64, float* weights, float* logits_out,
                         uint16_t* planes, int64_t tokens, int hidden, int experts, int topk,
                         hipStream_t stream) {
     if (tokens == 0) return MOE_OK;
     if (router_w != nullptr) {  // else planes already holds the split
-        const int64_t n = static_cast<int64_t>(experts) * hidden;
-        hipLaunchKernelGGL(router_split_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0,
-                           stream, router_w, planes, n);
-        const int rc = check_launch("router_split_kernel");
+        const int rc = launch_router_split(router_w, planes, experts, hidden, stream);
         if (rc != MOE_OK) return rc;
     }
     // Buffer offsets are 32-bit: 3*E*H*2 bytes of planes and 32 rows of x must fit.

@@ -130,6 +130,16 @@ class HipExtension:
             experts, topk, _stream(x.device))
         self.lib.check(status, "router_fused_out")
 
+    def router_split_out(self, router_weight, scratch):
+        """Write the bf16 split of ``router_weight`` [E,H] fp32 into ``scratch`` alone (no routing)."""
+        _check(router_weight.is_cuda and router_weight.is_contiguous() and router_weight.dim() == 2
+               and router_weight.dtype == torch.float32, "expected contiguous FP32 GPU router_weight[E,H]")
+        _check_gpu_tensor(scratch, router_weight, "scratch")
+        experts, hidden = router_weight.shape
+        status = self.lib.moe_router_split(_ptr(router_weight), _ptr(scratch), scratch.numel() * scratch.element_size(),
+                                           experts, hidden, _stream(router_weight.device))
+        self.lib.check(status, "router_split_out")
+
     # -- transport -----------------------------------------------------------
     def scratch_bytes(self, tokens, experts, topk):
         return int(self.lib.moe_dispatch_scratch_bytes(tokens, experts, topk))

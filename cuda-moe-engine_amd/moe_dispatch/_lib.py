@@ -13,7 +13,7 @@ from functools import lru_cache
 from pathlib import Path
 
 LIBRARY_NAME = "libmoe_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -31,6 +31,7 @@ _SIGNATURES = {
     "moe_topk_route": (_int, [_c_void_p] * 5 + [_i64, _i64, _i64, _c_void_p]),
     "moe_router_scratch_bytes": (_i64, [_i64, _i64]),
     "moe_router_fused": (_int, [_c_void_p] * 8 + [_i64] * 5 + [_c_void_p]),
+    "moe_router_split": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "moe_dispatch_scratch_bytes": (_i64, [_i64, _i64, _i64]),
     "moe_dispatch": (
         _int,

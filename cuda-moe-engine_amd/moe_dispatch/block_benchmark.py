@@ -7,7 +7,8 @@ Graph capture and replay of the MoE block forward:
 
 Mirrors ``capture_forward`` of the reference (``src/moe_dispatch/block_benchmark.py:48-64``):
 warm up on a side stream, capture one ``block(x)`` into a graph (a hipGraph under
-ROCm), replay it once and require the replay to reproduce the eager output.
+ROCm), replay it once and require the replay to reproduce the eager output. The
+graph leaves the router weights' split out (see ``ForwardGraph``).
 The reference accepts rtol = atol = 3e-2 here; every kernel of this package is
 deterministic, so the replay must match the eager forward bit for bit.
 
@@ -22,13 +23,40 @@ from __future__ import annotations
 import torch
 
 
+class ForwardGraph:
+    """A captured ``block(x)``: ``replay()`` runs it again on the current stream.
+
+    For ``cuda_fused`` blocks the graph reads the router weights' bf16 split
+    from the block's scratch instead of recomputing it (one kernel fewer per
+    replay); ``replay()`` first redoes the split, outside the graph, when the
+    router weights were replaced or written in place since the split was
+    taken, so every replay routes with the weights as they are. ``graph`` is
+    the underlying ``torch.cuda.CUDAGraph``: replaying it directly skips that
+    check.
+    """
+
+    def __init__(self, block, graph, output):
+        self.block = block
+        self.graph = graph
+        self.output = output
+
+    def replay(self):
+        block = self.block
+        if block.implementation == "cuda_fused" and block._router_scratch is not None:
+            key = block._router_split_key()
+            if not block._same_split(key, block._router_split_of):
+                block._extension.router_split_out(block.router_weight, block._router_scratch)
+                block._router_split_of = key
+        self.graph.replay()
+
+
 @torch.inference_mode()
 def capture_forward(block, x, warmup=3):
-    """Capture ``block(x)`` into a ``torch.cuda.CUDAGraph``; raises if the replay differs.
+    """Capture ``block(x)`` into a graph (a hipGraph under ROCm); raises if the replay differs.
 
-    The graph reads ``x`` and writes ``block.workspace(x).transport.output`` (the
-    tensor ``block(x)`` returns); keep ``x`` alive and update it in place to feed
-    new tokens of the same shape.
+    Returns a ``ForwardGraph``. The graph reads ``x`` and writes
+    ``block.workspace(x).transport.output`` (the tensor ``block(x)`` returns);
+    keep ``x`` alive and update it in place to feed new tokens of the same shape.
     """
     expected = block(x).clone()
     device = x.device
@@ -39,13 +67,18 @@ def capture_forward(block, x, warmup=3):
             block(x)
     torch.cuda.current_stream(device).wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        output = block(x)
-    graph.replay()
+    block._split_in_capture = False
+    try:
+        with torch.cuda.graph(graph, stream=stream):
+            output = block(x)
+    finally:
+        block._split_in_capture = True
+    forward = ForwardGraph(block, graph, output)
+    forward.replay()
     torch.cuda.synchronize(device)
     if not torch.equal(output, expected):
         raise RuntimeError("graph replay differs from the eager forward")
-    return graph
+    return forward
 
 
 IMPLEMENTATIONS = ("torch", "cuda", "cuda_fused")

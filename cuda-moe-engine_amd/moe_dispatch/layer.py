@@ -133,6 +133,7 @@ class MoEBlock(torch.nn.Module):
         self._route_buffers = {}
         self._router_scratch = None  # bf16 split of the router weights (fused router)
         self._router_split_of = None  # _router_split_key() of the weights the split holds
+        self._split_in_capture = True  # record the router split into captured graphs
         self._launches = {}  # cuda_fused: pre-validated launches per input signature
         self._extension = get_extension() if implementation != "torch" else None
 
@@ -165,22 +166,12 @@ class MoEBlock(torch.nn.Module):
                 need = self._extension.router_scratch_bytes(self.config.experts, self.config.hidden)
                 self._router_scratch = torch.empty(need, dtype=torch.uint8, device=x.device)
                 self._router_split_of = None
-            # The split of the router weights is redone only when they may have
-            # changed (another tensor, or an in-place write, which bumps the
-            # version counter), and always inside a graph capture, so that every
-            # replay of the graph reads the weights as they are then.
-            split_of = self._router_split_key()
-            capturing = _capturing()
-            if self._same_split(split_of, self._router_split_of) and not capturing:
-                router_weight = None
-            else:
-                router_weight = self.router_weight
+            router_weight, split_of = self._router_split_plan()
             self._extension.router_fused_out(
-                x, router_weight, self.routing_bias, ids32, ids64, weights,
-                scratch=self._router_scratch,
+                x, None if router_weight is None else self.router_weight, self.routing_bias, ids32, ids64,
+                weights, scratch=self._router_scratch,
             )
-            # A captured split runs only when the graph is replayed.
-            self._router_split_of = None if capturing else split_of
+            self._router_split_of = split_of
             return ids32, ids64, weights
         logits = torch.nn.functional.linear(x.float(), self.router_weight) + self.routing_bias
         selected, ids64 = torch.topk(logits, self.config.topk, dim=-1)
@@ -205,6 +196,24 @@ class MoEBlock(torch.nn.Module):
     @staticmethod
     def _same_split(a, b):
         return a is not None and b is not None and a[0] is b[0] and a[1:] == b[1:]
+
+    def _router_split_plan(self):
+        """(router weight pointer or None, split key to record) for the next fused-router call.
+
+        The bf16 split of the router weights is redone only when they may have
+        changed (another tensor, or an in-place write, which bumps the version
+        counter). Inside a graph capture it is recorded into the graph, so that
+        every replay reads the weights as they are then, unless the capture is
+        ``capture_forward``'s: its graph's replay() re-splits beforehand, and only
+        when the weights changed. A recorded split runs only when the graph is
+        replayed, so after recording one the split counts as stale.
+        """
+        split_of = self._router_split_key()
+        capturing = _capturing()
+        current = self._same_split(split_of, self._router_split_of)
+        if current and not (capturing and self._split_in_capture):
+            return None, split_of
+        return self.router_weight.data_ptr(), (None if capturing else split_of)
 
     def workspace(self, x):
         key = (x.shape[0], x.dtype, x.device)
@@ -334,14 +343,9 @@ class _FusedLaunches:
         lib = self.lib
         stream = current_stream_handle(self.device_index)
         x_ptr = x.data_ptr()
-        split_of = block._router_split_key()
-        capturing = _capturing()
-        if block._same_split(split_of, block._router_split_of) and not capturing:
-            router_weight = None
-        else:
-            router_weight = block.router_weight.data_ptr()
+        router_weight, split_of = block._router_split_plan()
         lib.check(lib.moe_router_fused(x_ptr, router_weight, *self.router, stream), "router_fused_out")
-        block._router_split_of = None if capturing else split_of
+        block._router_split_of = split_of
         lib.check(lib.moe_dispatch(x_ptr, *self.dispatch, stream), "dispatch")
         lib.check(lib.moe_grouped_gateup_swiglu(*self.gateup, stream), "gateup_swiglu_out")
         lib.check(lib.moe_grouped_gemm(*self.down, stream), "grouped_gemm_out")

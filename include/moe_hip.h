@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 4
+#define MOE_ABI_VERSION 5
 
 typedef enum {
     MOE_DTYPE_F32 = 0,
@@ -95,6 +95,16 @@ int moe_router_fused(const void* x, const float* router_w, const float* bias, in
                      int64_t* ids64, float* weights, float* logits_out, void* scratch,
                      int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
                      int64_t topk, void* stream);
+
+/*
+ * The bf16 split of router_w that moe_router_fused keeps in its scratch, alone:
+ * writes the planes a later moe_router_fused(router_w = NULL, ...) call reads.
+ * For callers that keep the split current outside a captured graph, so that
+ * replays of a forward captured with router_w = NULL do not redo it. No
+ * counterpart in the reference (its router has no such split).
+ */
+int moe_router_split(const float* router_w, void* scratch, int64_t scratch_bytes, int64_t experts,
+                     int64_t hidden, void* stream);
 
 /* Bytes of scratch moe_dispatch needs for (T, E, K). */
 int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk);
