@@ -368,15 +368,30 @@ struct RingOps {
     char* lds;
     int wave;
 
+    // A tile's two buffer resources: its rows of A, and the expert's weight rows
+    // from the tile's first column on (so the per-lane offsets below do not
+    // depend on the tile). Rows past the tile (or the expert) read as zero.
+    struct Rsrc {
+        __amdgpu_buffer_rsrc_t a, b;
+    };
+    static __device__ __forceinline__ Rsrc tile_rsrc(const GemmParams& p, int expert, int64_t col0, int64_t row0,
+                                                     int64_t row_end) {
+        const int64_t K = p.k;
+        const int64_t a_rows = min<int64_t>(row_end - row0, TM);
+        return Rsrc{make_rsrc(p.a + row0 * K, static_cast<uint32_t>(a_rows * K * 2)),
+                    make_rsrc(p.b + (static_cast<int64_t>(expert) * p.nb + col0) * K,
+                              static_cast<uint32_t>((p.nb - col0) * K * 2))};
+    }
+
     __device__ __forceinline__ RingOps(const GemmParams& p, char* lds_, int expert, int64_t col0,
                                        int64_t row0, int64_t row_end)
         : lds(lds_) {
         const int lane = threadIdx.x & 63;
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int64_t K = p.k;
-        const int64_t a_rows = min<int64_t>(row_end - row0, TM);
-        rsrc_a = make_rsrc(p.a + row0 * K, static_cast<uint32_t>(a_rows * K * 2));
-        rsrc_b = make_rsrc(p.b + static_cast<int64_t>(expert) * p.nb * K, static_cast<uint32_t>(p.nb * K * 2));
+        const Rsrc r = tile_rsrc(p, expert, col0, row0, row_end);
+        rsrc_a = r.a;
+        rsrc_b = r.b;
         // Load l of a stage covers LDS rows (wave * X_LOADS + l) * 8 + lane / 8.
         const int lrow = lane >> 3;
         const int pchunk = lane & 7;
@@ -394,36 +409,42 @@ struct RingOps {
             // tile and the matching up rows (I further on).
             const int wcol = r / WTN, w = r % WTN;
             static constexpr int HALF = WTN / 2;
-            const int64_t col = col0 + wcol * HALF + (w % HALF);
+            const int64_t col = wcol * HALF + (w % HALF);  // from the tile's first column
             brow = (w < HALF) ? col : p.n_out + col;
         } else {
-            brow = col0 + r;
+            brow = r;
         }
         b_off[i] = static_cast<uint32_t>((brow * K + (pchunk ^ ring_key(r)) * 8) * 2);
     }
     }
-    // Load l of stage kt into ring slot st, of A and of B.
-    __device__ __forceinline__ void issue_a(int kt, int st, int l) const {
-        dma16(rsrc_a, lds + st * A_STAGE + (wave * A_LOADS + l) * 1024, a_off[l],
-              static_cast<uint32_t>(kt) * kRowBytes);
+    // Load l of stage kt into ring slot st, of A and of B (of this tile, or of
+    // the tile whose resources are given).
+    __device__ __forceinline__ void issue_a(int kt, int st, int l) const { issue_a(rsrc_a, kt, st, l); }
+    __device__ __forceinline__ void issue_b(int kt, int st, int l) const { issue_b(rsrc_b, kt, st, l); }
+    __device__ __forceinline__ void issue_a(__amdgpu_buffer_rsrc_t r, int kt, int st, int l) const {
+        dma16(r, lds + st * A_STAGE + (wave * A_LOADS + l) * 1024, a_off[l], static_cast<uint32_t>(kt) * kRowBytes);
     }
-    __device__ __forceinline__ void issue_b(int kt, int st, int l) const {
-        dma16(rsrc_b, lds + B_BASE + st * B_STAGE + (wave * B_LOADS + l) * 1024, b_off[l],
+    __device__ __forceinline__ void issue_b(__amdgpu_buffer_rsrc_t r, int kt, int st, int l) const {
+        dma16(r, lds + B_BASE + st * B_STAGE + (wave * B_LOADS + l) * 1024, b_off[l],
               static_cast<uint32_t>(kt) * kRowBytes);
     }
     // The windows before stage 0, in the steady-state order (A of stage
-    // v+SA, then B of stage v+SB, for v = -SB .. -1). Stages past the last are
-    // loaded as the last one again, so every window issues the same loads and
-    // the vmcnt accounting stays uniform.
-    __device__ __forceinline__ void prologue(int k_steps) const {
+    // v+SA, then B of stage v+SB, for v = -SB .. -1; only v = -1 when `last`).
+    // Stage s goes to slots (a0 + s) % SA and (b0 + s) % SB. Stages past the
+    // last are loaded as the last one again, so every window issues the same
+    // loads and the vmcnt accounting stays uniform.
+    __device__ __forceinline__ void prologue(int k_steps, int a0 = 0, int b0 = 0, bool last = false) const {
 #pragma unroll
         for (int v = -SB; v < 0; ++v) {
+            if (last && v != -1) continue;
             if (v + SA >= 0) {
+                const int st = a0 + v + SA >= SA ? a0 + v : a0 + v + SA;
 #pragma unroll
-                for (int l = 0; l < A_LOADS; ++l) issue_a(min(v + SA, k_steps - 1), v + SA, l);
+                for (int l = 0; l < A_LOADS; ++l) issue_a(min(v + SA, k_steps - 1), st, l);
             }
+            const int st = b0 + v + SB >= SB ? b0 + v : b0 + v + SB;
 #pragma unroll
-            for (int l = 0; l < B_LOADS; ++l) issue_b(min(v + SB, k_steps - 1), v + SB, l);
+            for (int l = 0; l < B_LOADS; ++l) issue_b(min(v + SB, k_steps - 1), st, l);
         }
     }
 
@@ -448,10 +469,19 @@ struct NoHook {
 // before the first read instead of counting loads. hook: runs once the
 // k-loop is done and every wave has finished with the ring (it may refill
 // LDS), before the epilogue.
+//
+// Chaining (persistent kernels): the ring's stage s sits in slots (sa0 + s) % SA
+// and (sb0 + s) % SB. With `chain`, the windows that would reload this tile's
+// last stage instead load the next tile's first stages (resources `next`, a
+// tile of the same shape and k) into the slots that follow, so the next tile
+// starts at slots (sa0 + k_steps) % SA and (sb0 + k_steps) % SB and its hook
+// only issues the prologue's last window. Requires k_steps >= SB.
 template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end, bool own_prologue = true,
-                                          bool wait_all = false, const Hook& hook = Hook{}) {
+                                          bool wait_all = false, const Hook& hook = Hook{}, int sa0 = 0, int sb0 = 0,
+                                          bool chain = false,
+                                          typename RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC, MAXS>::Rsrc next = {}) {
     using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC, MAXS>;
     constexpr int WTM = R::WTM, WTN = R::WTN, FA = R::FA, FB = R::FB;
     constexpr int A_LOADS = R::A_LOADS, B_LOADS = R::B_LOADS;
@@ -464,8 +494,6 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     const int wn = wave % WC;
     const int64_t K = p.k;
     const R ops(p, lds, expert, col0, row0, row_end);
-    auto issue_a = [&](int kt, int st, int l) { ops.issue_a(kt, st, l); };
-    auto issue_b = [&](int kt, int st, int l) { ops.issue_b(kt, st, l); };
 
     // Per-lane fragment addresses: lane l reads row (l%16) of a fragment at k
     // chunk l/16 of the sub-step (all 32 k of it in one 16-byte read). Fragments
@@ -501,6 +529,11 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     //
     // One set of fragments (FA A + FB B) is live. A 32-k sub-step runs in two
     // halves: B fragments [0, FB/2) with every A fragment, then [FB/2, FB).
+    // Inside a half the MFMAs go A fragment by A fragment with the B fragments
+    // in snake order (forward for even A fragments, backward for odd ones), so
+    // consecutive MFMAs change one operand, never both: the kernel is power-
+    // limited, and the fewer operand bits toggle, the higher the clock it holds
+    // (measured on MI355X: 0.5-1.2% faster than restarting each row at B 0).
     // During the first half this sub-step's B fragments [FB/2, FB) are read
     // (their previous values were last used by the previous second half);
     // during the second half the next sub-step's A fragment i is read right
@@ -524,18 +557,19 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     // first quarter, B loads over the second and third.
     struct Refill {
         int kt_a, slot_a, kt_b, slot_b;
+        __amdgpu_buffer_rsrc_t ra, rb;  // this tile's or (chained) the next tile's
     };
     auto refill_at = [&](auto g_c, const Refill& r) {
         constexpr int g = decltype(g_c)::value;  // MFMA slot in the window
         static_for<A_LOADS>([&](auto l_c) {
             constexpr int l = decltype(l_c)::value;
             constexpr int slot = kQuarters ? l * HM / A_LOADS : l * 4 * HM / LOADS;
-            if constexpr (slot == g) issue_a(r.kt_a, r.slot_a, l);
+            if constexpr (slot == g) ops.issue_a(r.ra, r.kt_a, r.slot_a, l);
         });
         static_for<B_LOADS>([&](auto l_c) {
             constexpr int l = decltype(l_c)::value;
             constexpr int slot = kQuarters ? HM + l * 2 * HM / B_LOADS : (A_LOADS + l) * 4 * HM / LOADS;
-            if constexpr (slot == g) issue_b(r.kt_b, r.slot_b, l);
+            if constexpr (slot == g) ops.issue_b(r.rb, r.kt_b, r.slot_b, l);
         });
     };
     // First half: B [0, HB) x A, reading this sub-step's B [HB, FB) at `bh`.
@@ -544,7 +578,7 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         constexpr int q = decltype(q_c)::value;
         static_for<HM>([&](auto m_c) {
             constexpr int m = decltype(m_c)::value;
-            constexpr int i = m / HB, j = m % HB;
+            constexpr int i = m / HB, j = (i % 2) ? HB - 1 - m % HB : m % HB;  // snake order
             if constexpr (q >= 0) refill_at(std::integral_constant<int, q * HM + m>{}, rf);
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
             static_for<HB>([&](auto b_c) {
@@ -561,7 +595,7 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         constexpr int q = decltype(q_c)::value;
         static_for<HM>([&](auto m_c) {
             constexpr int m = decltype(m_c)::value;
-            constexpr int i = m / HB, j = HB + m % HB;
+            constexpr int i = m / HB, j = HB + ((i % 2) ? HB - 1 - m % HB : m % HB);  // snake order
             if constexpr (q >= 0) refill_at(std::integral_constant<int, q * HM + m>{}, rf);
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
             if constexpr (!last) {
@@ -576,7 +610,7 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     };
 
     const int k_steps = static_cast<int>(K / kStageK);
-    if (own_prologue) ops.prologue(k_steps);
+    if (own_prologue) ops.prologue(k_steps, sa0, sb0);
     if (wait_all)
         wait_vm_lgkm<0>();
     else
@@ -584,29 +618,36 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     ring_barrier();
     fence();
     // Sub-step 0's fragments, in the order the second half reads them.
+    const uint32_t a_first = sa0 * A_STAGE, b_first = sb0 * B_STAGE;
     static_for<HM>([&](auto m_c) {
         constexpr int m = decltype(m_c)::value;
         constexpr int i = m / HB;
         static_for<HB>([&](auto b_c) {
             constexpr int b = decltype(b_c)::value;
-            if constexpr (second_read_slot(b) == m) fb[b] = read_at(vb[0], b);
+            if constexpr (second_read_slot(b) == m) fb[b] = read_at(vb[0] + b_first, b);
         });
-        if constexpr (m % HB == HB - 1) fa[i] = read_at(va[0], i);
+        if constexpr (m % HB == HB - 1) fa[i] = read_at(va[0] + a_first, i);
     });
     // Stage 0 up to its last quarter, then per stage u: [barrier] the last
     // quarter of stage u (reading stage u+1), then the first three quarters of
     // stage u+1; this window refills the slots stage u just freed.
     using NoLoads = std::integral_constant<int, -1>;
     using More = std::false_type;
-    const Refill none{0, 0, 0, 0};
-    first_half(vb[0], NoLoads{}, none);
-    second_half(va[1], vb[1], More{}, NoLoads{}, none);
-    first_half(vb[1], NoLoads{}, none);
-    int sa = 0, sb = 0;  // ring slots of stage u
+    const Refill none{0, 0, 0, 0, ops.rsrc_a, ops.rsrc_b};
+    first_half(vb[0] + b_first, NoLoads{}, none);
+    second_half(va[1] + a_first, vb[1] + b_first, More{}, NoLoads{}, none);
+    first_half(vb[1] + b_first, NoLoads{}, none);
+    int sa = sa0, sb = sb0;  // ring slots of stage u
     for (int u = 0; u + 1 < k_steps; ++u) {
         const int na = sa + 1 == SA ? 0 : sa + 1;
         const int nb = sb + 1 == SB ? 0 : sb + 1;
-        const Refill rf{min(u + SA, k_steps - 1), sa, min(u + SB, k_steps - 1), sb};
+        // Stages past this tile's last: the next tile's first ones when
+        // chained, else this tile's last one again.
+        const bool a_next = chain && u + SA >= k_steps;
+        const bool b_next = chain && u + SB >= k_steps;
+        const Refill rf{a_next ? u + SA - k_steps : min(u + SA, k_steps - 1), sa,
+                        b_next ? u + SB - k_steps : min(u + SB, k_steps - 1), sb,
+                        a_next ? next.a : ops.rsrc_a, b_next ? next.b : ops.rsrc_b};
         const uint32_t a0 = va[0] + na * A_STAGE, a1 = va[1] + na * A_STAGE;
         const uint32_t b0 = vb[0] + nb * B_STAGE, b1 = vb[1] + nb * B_STAGE;
         fence();
@@ -917,27 +958,49 @@ __device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, co
     }
 }
 
-template <bool SWIGLU, typename Hook>
-__device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const RingWork& w, bool wait_all,
-                                         const Hook& hook) {
+// Runs tile `w` starting at ring slots (sa, sb) (updated for the next tile).
+// When the next tile `nxt` has the same ring shape and the k chain is long
+// enough, the two are chained (see ring_tile): `w`'s last windows load `nxt`'s
+// first stages and its hook issues only the prologue's last window. Otherwise
+// the hook issues `nxt`'s whole prologue at slots 0.
+template <int SMT, int BNT, bool SWIGLU>
+__device__ __forceinline__ void ring_run_shape(const GemmParams& p, char* lds, const RingWork& w,
+                                               const RingWork& nxt, bool wait_all, int& sa, int& sb) {
+    using R = RingOps<SMT, BNT, SWIGLU, kRingBytes>;
+    const int k_steps = static_cast<int>(p.k / kStageK);
+    // Wave-uniform (it selects buffer resources, which live in SGPRs).
+    const bool chain = __builtin_amdgcn_readfirstlane(nxt.valid && nxt.variant == w.variant && k_steps >= R::SB) != 0;
+    typename R::Rsrc next{};
+    if (chain) next = R::tile_rsrc(p, nxt.expert, nxt.col0, nxt.row0, nxt.row_end);
+    const int na = (sa + k_steps) % R::SA, nb = (sb + k_steps) % R::SB;
+    auto hook = [&] {
+        if (!nxt.valid) return;
+        if (chain)
+            R(p, lds, nxt.expert, nxt.col0, nxt.row0, nxt.row_end).prologue(k_steps, na, nb, true);
+        else
+            ring_prologue<SWIGLU>(p, lds, nxt);
+    };
+    ring_tile<SMT, BNT, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook,
+                                             sa, sb, chain, next);
+    sa = chain ? na : 0;
+    sb = chain ? nb : 0;
+}
+
+template <bool SWIGLU>
+__device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const RingWork& w, const RingWork& nxt,
+                                         bool wait_all, int& sa, int& sb) {
     switch (w.variant) {
-        case 0: ring_tile<4, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook); break;
-        case 1: ring_tile<2, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook); break;
-        case 2: ring_tile<1, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook); break;
+        case 0: ring_run_shape<4, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 1: ring_run_shape<2, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 2: ring_run_shape<1, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         default:
             if constexpr (!SWIGLU) {
-                if (w.variant == 3)
-                    ring_tile<4, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
-                else if (w.variant == 4)
-                    ring_tile<2, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
-                else if (w.variant == 5)
-                    ring_tile<1, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
-                else if (w.variant == 6)
-                    ring_tile<4, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
-                else if (w.variant == 7)
-                    ring_tile<2, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
-                else
-                    ring_tile<1, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook);
+                if (w.variant == 3) ring_run_shape<4, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 4) ring_run_shape<2, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 5) ring_run_shape<1, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 6) ring_run_shape<4, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 7) ring_run_shape<2, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else ring_run_shape<1, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
             }
     }
 }
@@ -965,25 +1028,26 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
     if (!cur.valid) return;
     ring_prologue<SWIGLU>(p, lds, cur);
     bool after_epilogue = false;
+    int sa = 0, sb = 0;  // ring slots of the current tile's first stage
     for (;;) {
         int qn = q, sn = sub + 1;
-        const RingWork nxt = next(qn, sn);
-        auto hook = [&] {
-            if (!nxt.valid) return;
-            // Opaque copies: nothing derived from the next tile may be hoisted
-            // into (and kept live through) the current tile's k-loop.
-            RingWork w = nxt;
-            int r0 = static_cast<int>(w.row0), r1 = static_cast<int>(w.row_end), c = static_cast<int>(w.col0);
-            int e = w.expert, v = w.variant;
+        RingWork nxt = next(qn, sn);
+        // Wave-uniform, opaque copies: nothing derived from the next tile may be
+        // hoisted into (and kept live through) the current tile's k-loop.
+        {
+            int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(nxt.row0));
+            int r1 = __builtin_amdgcn_readfirstlane(static_cast<int>(nxt.row_end));
+            int c = __builtin_amdgcn_readfirstlane(static_cast<int>(nxt.col0));
+            int e = __builtin_amdgcn_readfirstlane(nxt.expert), v = __builtin_amdgcn_readfirstlane(nxt.variant);
+            nxt.valid = __builtin_amdgcn_readfirstlane(nxt.valid ? 1 : 0) != 0;
             asm volatile("" : "+s"(r0), "+s"(r1), "+s"(c), "+s"(e), "+s"(v));
-            w.row0 = r0;
-            w.row_end = r1;
-            w.col0 = c;
-            w.expert = e;
-            w.variant = v;
-            ring_prologue<SWIGLU>(p, lds, w);
-        };
-        ring_run<SWIGLU>(p, lds, cur, after_epilogue, hook);
+            nxt.row0 = r0;
+            nxt.row_end = r1;
+            nxt.col0 = c;
+            nxt.expert = e;
+            nxt.variant = v;
+        }
+        ring_run<SWIGLU>(p, lds, cur, nxt, after_epilogue, sa, sb);
         if (!nxt.valid) break;
         cur = nxt;
         q = qn;

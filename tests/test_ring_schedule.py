@@ -108,3 +108,93 @@ def test_small_tiles_get_equal_depths():
     assert replay(64, 64, 3 * 128 * ROW_BYTES, 8) == (3, 3)
     assert replay(64, 256, 160 * KIB, 8) == (4, 4)
     assert replay(64, 32, 160 * KIB, 8, cap=8) == (8, 8)
+
+
+def replay_chain(tm, bnt, lds, k_steps, tiles=3, cap=4):
+    """Consecutive tiles of one shape chained as the persistent kernel does.
+
+    Tile t's stage s sits in slots (a0 + s) % SA and (b0 + s) % SB. Its last
+    windows, which would reload its last stage, load the next tile's first
+    stages into the slots that follow; after its k-loop (every wave done with
+    the ring) the hook issues the prologue's last window of the next tile, which
+    then waits for all loads before its first read. Checks that every read
+    stage has landed, that no load overwrites a slot whose stage is still to be
+    read, and that the next tile finds its stages where it looks for them.
+    """
+    a_stage, b_stage = tm * ROW_BYTES, bnt * ROW_BYTES
+    sb, sa = b_stages(a_stage, b_stage, lds, cap), a_stages(a_stage, b_stage, lds, cap)
+    assert k_steps >= sb
+    a_loads, b_loads = tm // 32, bnt // 32
+    loads = a_loads + b_loads
+    vm_steady = (b_loads if sb > sa else 0) + (sa - 2) * loads
+    issued = []  # [matrix, tile, stage, slot, done]
+    slot_holds = {("A", i): None for i in range(sa)} | {("B", i): None for i in range(sb)}  # (tile, stage)
+
+    def issue(matrix, tile, stage, slot, n):
+        held = slot_holds[(matrix, slot)]
+        # the slot's previous stage must already have been read (consumed)
+        assert held is None or held in consumed, (matrix, tile, stage, slot, held)
+        slot_holds[(matrix, slot)] = (tile, stage)
+        issued.extend([[matrix, tile, stage, slot, False] for _ in range(n)])
+
+    def wait(n):
+        for entry in issued[: max(len(issued) - n, 0)]:
+            entry[4] = True
+
+    def landed(matrix, tile, stage, slot):
+        # the loads of this stage into the slot it is read from (the last tile's
+        # reloads of its last stage go to other slots and are never read)
+        mine = [e for e in issued if e[:4] == [matrix, tile, stage, slot]]
+        return bool(mine) and all(e[4] for e in mine) and slot_holds[(matrix, slot)] == (tile, stage)
+
+    consumed = set()
+    a0 = b0 = 0
+    for v in range(-sb, 0):  # tile 0's full prologue at slots 0
+        if v + sa >= 0:
+            issue("A", 0, v + sa, (v + sa) % sa, a_loads)
+        issue("B", 0, v + sb, (v + sb) % sb, b_loads)
+    for t in range(tiles):
+        chain = t + 1 < tiles
+        wait(0)  # the first wait of a tile after an epilogue (or the kernel's first) takes everything
+        assert landed("A", t, 0, a0 % sa) and landed("B", t, 0, b0 % sb)
+        for u in range(k_steps - 1):
+            if u > 0:
+                wait(vm_steady)
+            assert landed("A", t, u + 1, (a0 + u + 1) % sa) and landed("B", t, u + 1, (b0 + u + 1) % sb)
+            consumed.add((t, u))  # stage u's last reads happen before this window's refills
+            sa_slot, sb_slot = (a0 + u) % sa, (b0 + u) % sb
+            for matrix, depth, slot, n in (("A", sa, sa_slot, a_loads), ("B", sb, sb_slot, b_loads)):
+                stage = u + depth
+                if stage < k_steps:
+                    issue(matrix, t, stage, slot, n)
+                elif chain:
+                    issue(matrix, t + 1, stage - k_steps, slot, n)
+                else:  # the last tile reloads its last stage into a freed slot (never read)
+                    slot_holds[(matrix, slot)] = None
+                    issued.extend([[matrix, t, k_steps - 1, slot, False] for _ in range(n)])
+        consumed.add((t, k_steps - 1))
+        if not chain:
+            break
+        a0, b0 = (a0 + k_steps) % sa, (b0 + k_steps) % sb
+        # hook: the prologue's last window of the next tile (A stage SA-1, B stage SB-1)
+        issue("A", t + 1, sa - 1, (a0 + sa - 1) % sa, a_loads)
+        issue("B", t + 1, sb - 1, (b0 + sb - 1) % sb, b_loads)
+        for s in range(sa):
+            assert slot_holds[("A", (a0 + s) % sa)] == (t + 1, s)
+        for s in range(sb):
+            assert slot_holds[("B", (b0 + s) % sb)] == (t + 1, s)
+    return sa, sb
+
+
+@pytest.mark.parametrize("tm,bnt", [(256, 256), (128, 256), (64, 256), (256, 128), (128, 128), (64, 128),
+                                    (256, 64), (128, 64), (64, 64)])
+def test_chained_tiles_find_their_stages(tm, bnt):
+    for k_steps in (4, 5, 7, 16, 64, 65):
+        replay_chain(tm, bnt, 160 * KIB, k_steps)
+
+
+def test_chained_start_slots_follow_the_k_chain():
+    """k_steps = 5 on the full tile (SA = 2, SB = 3): the next tile starts at A slot 1
+    and B slot 2, not 0; the replay above checks it finds its stages there."""
+    sa, sb = replay_chain(256, 256, 160 * KIB, 5, tiles=2)
+    assert (sa, sb) == (2, 3) and (0 + 5) % sa == 1 and (0 + 5) % sb == 2
