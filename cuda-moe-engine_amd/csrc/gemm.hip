@@ -670,42 +670,61 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         hook();
     }
 
-    // Epilogue: one row per lane, four consecutive columns per 8-byte store.
+    // Epilogue. Lane l holds, in each 16 x 16 block, row l%16 and columns
+    // 4*(l/16) + 0..3. For each pair of neighbouring blocks a
+    // v_permlane16_swap per dword exchanges data between lane rows 0<->1 and
+    // 2<->3 (lanes 16 apart hold the same output row), after which lane row g
+    // holds the 8 consecutive columns 8 * (0, 2, 1, 3)[g] of the pair's 32:
+    // one 16-byte store where there were two 8-byte ones, and each store
+    // instruction writes 64 contiguous bytes per output row instead of 32.
     // Each row of accumulators is first moved to VGPRs through an empty asm
     // operand: without it the register allocator shapes the accumulators' AGPR
     // assignment after the epilogue's register pairs and copies them inside the
-    // k-loop on every step.
-    const int col4 = 4 * (lane >> 4);
+    // k-loop on every step. The swaps run on every lane (before the row test).
+    const int lane_row = lane >> 4;
+    const int col4 = 4 * lane_row;
+    const int col8 = 8 * (((lane_row & 1) << 1) | (lane_row >> 1));
+    // Blocks b0 and b0 + 1 of a row fragment, as four bf16 each, into crow from
+    // column `base` (the first column of block b0).
+    auto store_pair = [&](uint16_t* crow, bool row_ok, int64_t base, uint2 x, uint2 y) {
+        const auto s0 = __builtin_amdgcn_permlane16_swap(x.x, y.x, false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(x.y, y.y, false, false);
+        const int64_t col = base + col8;
+        if (row_ok && col < p.n_out)
+            *reinterpret_cast<uint4*>(crow + col) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+    };
+    auto store_one = [&](uint16_t* crow, bool row_ok, int64_t base, uint2 x) {
+        const int64_t col = base + col4;
+        if (row_ok && col < p.n_out) *reinterpret_cast<uint2*>(crow + col) = x;
+    };
+    constexpr int OUT_BLOCKS = SWIGLU ? FB / 2 : FB;  // 16-column output blocks per wave
 #pragma unroll
     for (int i = 0; i < FA; ++i) {
 #pragma unroll
         for (int j = 0; j < FB; ++j) asm volatile("" : "+v"(acc[i][j]));
         const int64_t grow = row0 + wm * WTM + i * 16 + (lane & 15);
-        if (grow >= row_end) continue;
-        uint16_t* crow = p.c + grow * p.ldc;
-        if constexpr (SWIGLU) {
+        const bool row_ok = grow < row_end;
+        uint16_t* crow = p.c + (row_ok ? grow : row0) * p.ldc;
+        const int64_t first_col = col0 + wn * (SWIGLU ? WTN / 2 : WTN);
+        uint2 out[OUT_BLOCKS];
 #pragma unroll
-            for (int j = 0; j < FB / 2; ++j) {
-                const int64_t col = col0 + wn * (WTN / 2) + j * 16 + col4;
-                if (col >= p.n_out) continue;
+        for (int j = 0; j < OUT_BLOCKS; ++j) {
+            if constexpr (SWIGLU) {
                 float act[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const uint32_t gu = pack_bf16x2(acc[i][j][t], acc[i][j + FB / 2][t]);
                     act[t] = swiglu_fast(__uint_as_float(gu << 16), __uint_as_float(gu & 0xffff0000u));
                 }
-                *reinterpret_cast<uint2*>(crow + col) =
-                    make_uint2(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]));
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < FB; ++j) {
-                const int64_t col = col0 + wn * WTN + j * 16 + col4;
-                if (col >= p.n_out) continue;
-                *reinterpret_cast<uint2*>(crow + col) =
-                    make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
+                out[j] = make_uint2(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]));
+            } else {
+                out[j] = make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
             }
         }
+#pragma unroll
+        for (int j = 0; j + 1 < OUT_BLOCKS; j += 2) store_pair(crow, row_ok, first_col + j * 16, out[j], out[j + 1]);
+        if constexpr (OUT_BLOCKS % 2 == 1)
+            store_one(crow, row_ok, first_col + (OUT_BLOCKS - 1) * 16, out[OUT_BLOCKS - 1]);
     }
 }
 
