@@ -753,8 +753,13 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
 // For the plain GEMM a short last round (at most half of the slots busy) of
 // phase 1 (when there is no phase 2) or of the leftover phase-2 tiles is split
 // into 128-column pieces, and leftover phase-2 tiles into 64-column quarters
-// when at most a quarter of the slots would be busy. Every tile or piece runs its whole k chain in order
-// on one workgroup, so results do not depend on the schedule or on G.
+// when at most a quarter of the slots would be busy. When phase 1 fills at
+// most half of the slots of one round beside a phase 2, its tiles run as
+// 128-column halves (the two halves of a tile in neighbouring slots of one
+// XCD, sharing the A slab in L2): at H=1024, I=2048, E=16, 4096 tokens the
+// down GEMM's 128 full tiles otherwise took one whole K=2048 chain on half of
+// the CUs. Every tile or piece runs its whole k chain in order on one
+// workgroup, so results do not depend on the schedule or on G.
 struct RingPhase {
     int count;   // tiles
     int main;    // tiles mapped XCD-contiguously
@@ -780,6 +785,8 @@ __device__ __forceinline__ RingPhase ring_phase(int count, int grid, bool allow_
 struct RingPlan {
     int n1;           // phase-1 tiles
     int n2;           // phase-2 tiles
+    bool half1;       // phase 1 runs as 128-column halves in the rounds
+    int u1;           // phase-1 units of the rounds (tiles, or halves)
     int per1;         // phase-1 tiles per XCD range
     int cpr;          // phase-1 tiles per XCD and round
     int rounds;       // interleaved rounds (0: none)
@@ -796,8 +803,10 @@ __device__ __forceinline__ RingPlan ring_plan(int n1, int n2, int grid, bool all
     RingPlan pl{};
     pl.n1 = n1;
     pl.n2 = n2;
+    pl.half1 = allow_split && n2 > 0 && n1 > 0 && 2 * n1 <= grid;
+    pl.u1 = pl.half1 ? 2 * n1 : n1;
     if (n2 > 0 && n1 > 0) {
-        pl.per1 = (n1 + kNumXcd - 1) / kNumXcd;
+        pl.per1 = (pl.u1 + kNumXcd - 1) / kNumXcd;
         int rounds = (pl.per1 + grid / kNumXcd - 1) / (grid / kNumXcd);
         if (n2 - 2 * (rounds * grid - kNumXcd * pl.per1) > grid) ++rounds;
         pl.rounds = rounds;
@@ -831,8 +840,8 @@ __device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int 
         const int j = (pos / kNumXcd + r * (per_xcd - pl.cpr)) % per_xcd;
         const int cols = r < pl.full_rounds ? pl.cpr : (r == pl.full_rounds ? pl.last_cols : 0);
         if (j < cols) {
-            const int tile = (pos % kNumXcd) * pl.per1 + r * pl.cpr + j;
-            if (tile < pl.n1) s = RingSlot{0, tile, -1, 1};
+            const int unit = (pos % kNumXcd) * pl.per1 + r * pl.cpr + j;
+            if (unit < pl.u1) s = pl.half1 ? RingSlot{0, unit >> 1, unit & 1, 1} : RingSlot{0, unit, -1, 1};
             return s;
         }
         // A phase-2 slot: its index among the rounds' phase-2 slots, in q order.
@@ -1274,7 +1283,10 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
         int64_t grid = device_cu_count();
         const int limit = g_gemm_workgroup_limit.load(std::memory_order_relaxed);
         if (limit > 0 && limit < grid) grid = limit;
-        if (blocks < grid) grid = blocks;
+        // At most one workgroup per unit of work: tiles, or for the plain GEMM
+        // the halves and quarters the plan may split them into.
+        const int64_t units = SWIGLU ? blocks : 4 * blocks;
+        if (units < grid) grid = units;
         grid = grid / kNumXcd * kNumXcd;
         if (grid < kNumXcd) grid = kNumXcd;
         hipLaunchKernelGGL((grouped_gemm_persistent_kernel<SWIGLU>), dim3(static_cast<unsigned>(grid)),

@@ -83,8 +83,8 @@ SCHEDULE_CASES = [
     # counts, alignment, output columns (N, or I for gate/up), k, gate/up?, workgroup bounds.
     # With 8-40 workgroups these small launches take every path of the persistent plan:
     # slots carrying two short tiles, an extra round, leftovers after the rounds, split
-    # halves and quarters, a partial last round (tests/test_ring_plan.py checks which
-    # case reaches which).
+    # halves and quarters, a partial last round, phase 1 as halves in the rounds
+    # (tests/test_ring_plan.py checks which case reaches which).
     ([300, 700, 3, 260, 40, 1, 129, 520], 8, 512, 128, False, (8, 24)),
     ([300, 700, 3, 260, 40, 1, 129, 520], 8, 512, 128, True, (8, 16, 40)),
     ([1030, 20, 5, 257, 64, 600, 0, 90], 8, 1024, 192, False, (8, 16, 40)),
@@ -93,6 +93,8 @@ SCHEDULE_CASES = [
     # 32 full tiles in whole rounds, 4 short ones left over: 64-column quarters at
     # 16 workgroups, 128-column halves at 8
     ([1030, 1030, 2048], 8, 512, 128, False, (8, 16)),
+    # 6 full tiles beside 4 short ones: halves in the rounds from 16 workgroups on
+    ([300, 40, 512], 8, 512, 128, False, (8, 16, 40)),
 ]
 
 

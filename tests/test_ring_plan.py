@@ -6,7 +6,9 @@ row tiles (phase 1) run in 8 XCD-contiguous ranges, cpr per XCD and round;
 the other slots of the rounds carry one or two of the experts' short last row
 tiles (phase 2); phase-2 tiles the rounds do not take, or phase 1 when there is
 no phase 2, run after the rounds with an optional split of a short last round
-into 128-column pieces (plain GEMM only). This restates those formulas and
+into 128-column pieces (plain GEMM only); a phase 1 that fills at most half of
+one round beside a phase 2 runs in the rounds as 128-column halves (plain GEMM
+only). This restates those formulas and
 checks that every tile (or both halves of a split tile) is assigned exactly
 once for random expert layouts and grid sizes, that the rounds keep each XCD's
 phase-1 tiles in order, and that the measured shapes get the intended plans.
@@ -39,10 +41,11 @@ def ring_phase(count, grid, allow_split, short_tiles=False):
 
 
 def ring_plan(n1, n2, grid, allow_split):
-    pl = {"n1": n1, "n2": n2, "per1": 0, "cpr": 0, "rounds": 0, "full_rounds": 0, "last_cols": 0,
-          "slots": 0, "carried": 0}
+    half1 = allow_split and n2 > 0 and n1 > 0 and 2 * n1 <= grid
+    pl = {"n1": n1, "n2": n2, "half1": half1, "u1": 2 * n1 if half1 else n1, "per1": 0, "cpr": 0, "rounds": 0,
+          "full_rounds": 0, "last_cols": 0, "slots": 0, "carried": 0}
     if n2 > 0 and n1 > 0:
-        per1 = (n1 + XCD - 1) // XCD
+        per1 = (pl["u1"] + XCD - 1) // XCD
         rounds = (per1 + grid // XCD - 1) // (grid // XCD)
         if n2 - 2 * (rounds * grid - XCD * per1) > grid:
             rounds += 1
@@ -64,8 +67,10 @@ def ring_slot(pl, grid, q, sub):
         j = (pos // XCD + r * (per_xcd - pl["cpr"])) % per_xcd  # rotated per round
         cols = pl["cpr"] if r < pl["full_rounds"] else (pl["last_cols"] if r == pl["full_rounds"] else 0)
         if j < cols:
-            tile = (pos % XCD) * pl["per1"] + r * pl["cpr"] + j
-            return (0, tile, -1) if sub == 0 and tile < pl["n1"] else None
+            unit = (pos % XCD) * pl["per1"] + r * pl["cpr"] + j
+            if sub or unit >= pl["u1"]:
+                return None
+            return (0, unit // 2, unit % 2) if pl["half1"] else (0, unit, -1)
         per_round = grid - XCD * pl["cpr"]
         if r <= pl["full_rounds"]:
             idx = r * per_round
@@ -123,12 +128,13 @@ def check_cover(n1, n2, grid, allow_split):
     assert all(phase == 1 for (phase, _), p in parts.items() if p == {4, 5, 6, 7})
     assert not (pl["carried"] and not allow_split and pl["rest"]["pieces"])
     # In the rounds, the workgroups of XCD x (those with blockIdx % 8 == x) run
-    # exactly phase-1 range x, each round's tiles before the next round's.
+    # exactly phase-1 range x (of tiles, or of halves), each round's before the next round's.
     for x in range(XCD):
-        ranged = sorted((q // grid, s[1]) for seq in runs[x::XCD] for q, s in seq
-                        if s[0] == 0 and q < pl["rounds"] * grid)
+        ranged = sorted((q // grid, 2 * s[1] + s[2] if pl["half1"] else s[1]) for seq in runs[x::XCD]
+                        for q, s in seq if s[0] == 0 and q < pl["rounds"] * grid)
         first = x * pl["per1"]
-        assert [t for _, t in ranged] == list(range(first, min(first + pl["per1"], n1)))
+        assert [t for _, t in ranged] == list(range(first, min(first + pl["per1"], pl["u1"])))
+    assert not pl["half1"] or allow_split
     return pl, runs
 
 
@@ -167,8 +173,10 @@ def test_grid_sizes_used_on_the_gpu_cover_each_path():
                 reached.add("partial last round")
             if pl["rounds"] > (pl["per1"] + grid // XCD - 1) // (grid // XCD):
                 reached.add("extra round")
+            if pl["half1"]:
+                reached.add("halves in the rounds")
     assert reached == {"two tiles in a slot", "leftover after the rounds", "pieces", "quarters",
-                       "partial last round", "extra round"}
+                       "partial last round", "extra round", "halves in the rounds"}
 
 
 def test_phase2_slots_rotate_over_the_cus():
@@ -189,6 +197,12 @@ def test_measured_shapes_get_the_intended_plans():
     # the short tiles run last as 256 quarters, one per workgroup.
     pl = ring_plan(*phase_counts(c4, 8, 16), 256, True)
     assert (pl["rounds"], pl["carried"], pl["rest"]["pieces"], pl["rest"]["ways"]) == (2, 0, 256, 4)
+    # H=1024, I=2048, E=16, 4096 tokens, down GEMM (4 column tiles): 128 full
+    # tiles run as 256 halves in one round; the short tiles follow as quarters.
+    c3 = [510, 525, 498, 530, 515, 505, 520, 490, 512, 507, 533, 495, 516, 511, 522, 503]
+    pl = ring_plan(*phase_counts(c3, 8, 4), 256, True)
+    assert (pl["half1"], pl["u1"], pl["rounds"], pl["carried"], pl["rest"]["ways"]) == (True, 256, 1, 0, 4)
+    assert not ring_plan(*phase_counts(c3, 8, 8), 256, False)["half1"]  # its gate/up GEMM: never split
     # No short tiles: phase 1 alone, as before.
     pl = ring_plan(*phase_counts([1024] * 8, 8, 112), 256, False)
     assert (pl["rounds"], pl["rest"]["blocks"]) == (0, 3584)
