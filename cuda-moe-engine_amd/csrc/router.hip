@@ -442,6 +442,176 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
     }
 }
 
+// Fused router for E <= 16 on loads straight into VGPRs (no LDS ring).
+//
+// Operands reach VGPRs through buffer loads, already in MFMA fragment layout
+// (lane l supplies row l%16 and k 8*(l/16) .. +7 of a 16 x 32 operand). Each
+// 16x16x32 product covers 8 tokens and a 64-k step: operand row 2t + h is
+// token t's k half h (k0 + 32h ..), so the eight lanes of a token read one
+// whole 128-byte line and a token load reads 8 full lines; a layout with one
+// token per row reads 64 bytes of 16 lines, and took 1.4x longer at H=4096,
+// 4096 tokens. The weight operand's column 2r + h holds plane row r (r = q*E
+// + e: plane q, expert e) at k half h, so output (2t + h, 2r + h) is token t's
+// k-half-h product with plane row r (the other outputs mix the halves and are
+// not used). The planes are read from a copy in this fragment order
+// (router_fragment_kernel): per 64-k step, F = ceil(6E/16) fragments of 1 KiB,
+// lane l's 16 bytes at byte 16*l, rows >= 3E zero, so a weight load reads 1
+// KiB of contiguous, fully used lines. Each (token group, fragment) pair has
+// its own accumulator; per token and plane row the block sums the halves and
+// the waves in order, and the logit is (lo + mid) + hi.
+//
+// A block owns 16 tokens (two groups of 8); its eight waves split the 64-k
+// steps into eight contiguous ranges of at most PER. The range is unrolled at
+// compile time with the loads D steps ahead of the multiplies, so the code is
+// straight-line and the compiler's wait before each multiply counts only the
+// loads issued after that step's (a runtime loop carried the in-flight
+// fragments through register copies that waited for every load). Lanes of
+// steps past the wave's range and of k past `hidden` read zero through an
+// out-of-range offset, with no memory traffic.
+//
+// Why no LDS ring here: the ring kernel moved every operand byte through
+// direct-to-LDS loads, 8 KiB per 64-k stage for 16 tokens (x, the planes and
+// the zero rows of unused expert slots), and at H=4096, 4096 tokens its time
+// did not move when either the x or the plane loads were replaced by
+// out-of-range (zero, no traffic) ones: 12.3 us.
+constexpr int kDirectWaves = 8;
+constexpr int kDirectMaxPer = 16;   // 64-k steps per wave: hidden <= 8 * 16 * 64 = 8192
+constexpr int kDirectMaxExperts = 16;
+
+__host__ __device__ constexpr int router_fragments(int experts) { return (6 * experts + 15) / 16; }
+
+// Plane fragments from the row-major planes ([3][E][H] bf16): one thread per
+// 16-byte lane chunk (64-k step s, fragment f, lane l = (column n, k chunk kq)).
+__global__ __launch_bounds__(256) void router_fragment_kernel(const uint16_t* __restrict__ planes,
+                                                              uint16_t* __restrict__ frags, int experts,
+                                                              int hidden, int64_t chunks) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= chunks) return;
+    const int F = router_fragments(experts);
+    const int lane = static_cast<int>(i & 63);
+    const int64_t sf = i >> 6;
+    const int f = static_cast<int>(sf % F);
+    const int64_t s = sf / F;
+    const int c = f * 16 + (lane & 15);
+    const int r = c >> 1, h = c & 1;
+    const int64_t k = s * 64 + h * 32 + (lane >> 4) * 8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (r < 3 * experts && k < hidden) v = *reinterpret_cast<const uint4*>(planes + r * static_cast<int64_t>(hidden) + k);
+    *reinterpret_cast<uint4*>(frags + i * 8) = v;
+}
+
+typedef uint32_t ru32x4_t __attribute__((ext_vector_type(4)));
+
+// Loads in flight ahead of the multiplies: about 48 (vmcnt holds 63), and
+// fewer steps when the fragments are many (VGPRs).
+template <int PER, int F>
+constexpr int direct_depth() {
+    constexpr int d = F > 3 ? 4 : 48 / (2 + F);
+    return d < PER ? d : PER;
+}
+
+template <int PER, int F>
+__global__ __launch_bounds__(kDirectWaves * 64) void router_direct_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ frags, const float* __restrict__ bias,
+    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, float* __restrict__ weights,
+    float* __restrict__ logits_out, int64_t tokens, int hidden, int experts, int topk) {
+    constexpr int TB = kRouterTokens, PR = 8 * F, PRP = 2 * PR + 1;
+    constexpr int D = direct_depth<PER, F>();
+    __shared__ float part[kDirectWaves][TB][PRP];  // [wave][token][half * PR + plane row]
+    __shared__ float sbias[kDirectMaxExperts];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TB;
+    const int64_t rows = min(static_cast<int64_t>(TB), tokens - t0);
+    const uint32_t row_bytes = static_cast<uint32_t>(hidden) * 2;
+    const int steps = (hidden + 63) / 64;
+    const __amdgpu_buffer_rsrc_t rsrc_x = make_rsrc(x + t0 * hidden, static_cast<uint32_t>(rows) * row_bytes);
+    const __amdgpu_buffer_rsrc_t rsrc_f = make_rsrc(frags, static_cast<uint32_t>(steps) * F * 1024u);
+    const int per = (steps + kDirectWaves - 1) / kDirectWaves;  // <= PER (the launcher's choice)
+    const int s_begin = min(steps, wave * per);
+    const int s_end = min(steps, s_begin + per);
+    const int m = lane & 15, kq = lane >> 4, h = m & 1;
+    const int k_lane = h * 32 + kq * 8;  // this lane's k inside a step
+    const uint32_t x_off = static_cast<uint32_t>(m >> 1) * row_bytes + k_lane * 2;
+
+    struct Frag {
+        ru32x4_t a[2], b[F];
+    };
+    auto load = [&](int s, Frag& fr) {
+        const bool in = s < s_end;
+        const bool k_in = in && s * 64 + k_lane < hidden;
+        const uint32_t k_bytes = static_cast<uint32_t>(s) * 128;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+            fr.a[g] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsrc_x, k_in ? x_off + g * 8 * row_bytes + k_bytes : kRouterOob, 0, 0);
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            fr.b[f] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsrc_f, in ? static_cast<uint32_t>((s * F + f) * 64 + lane) * 16 : kRouterOob, 0, 0);
+    };
+    rfloatx4_t acc[2][F];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc[g][f] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
+    Frag fr[D];
+    static_for<D>([&](auto u_c) { load(s_begin + decltype(u_c)::value, fr[decltype(u_c)::value]); });
+    static_for<PER>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int f = 0; f < F; ++f)
+                acc[g][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rbf16x8_t, fr[i % D].a[g]),
+                                                                    __builtin_bit_cast(rbf16x8_t, fr[i % D].b[f]),
+                                                                    acc[g][f], 0, 0, 0);
+        if constexpr (i + D < PER) load(s_begin + i + D, fr[i % D]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    // 16x16 results: lane l holds operand rows 4*(l/16) + j and column c = 16f
+    // + l%16; the useful ones have the row's half equal to the column's (j % 2
+    // == c % 2): token 8g + 2*(l/16) + j/2, plane row c/2, half c%2.
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int j = 2 * jj + h;
+                part[wave][8 * g + 2 * kq + jj][h * PR + 8 * f + (m >> 1)] = acc[g][f][j];
+            }
+    if (threadIdx.x < experts) sbias[threadIdx.x] = bias[threadIdx.x];
+    __syncthreads();
+    constexpr int EPL = kDirectMaxExperts / 8;
+    const int tl = wave * 8 + (lane >> 3);
+    const int sub = lane & 7;
+    const int64_t token = t0 + tl;
+    if (tl < TB && token < tokens) {  // uniform across each group of eight lanes
+        float v[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = sub * EPL + j;
+            v[j] = -INFINITY;
+            if (e < experts) {
+                float q[3];
+#pragma unroll
+                for (int p = 0; p < 3; ++p) {
+                    const int pr = p * experts + e;
+                    float sum = part[0][tl][pr] + part[0][tl][PR + pr];
+#pragma unroll
+                    for (int w = 1; w < kDirectWaves; ++w) sum = sum + (part[w][tl][pr] + part[w][tl][PR + pr]);
+                    q[p] = sum;
+                }
+                const float logit = (q[2] + q[1]) + q[0];
+                if (logits_out) logits_out[token * experts + e] = logit;
+                v[j] = logit + sbias[e];
+            }
+        }
+        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights);
+    }
+}
+
 // Sum of a token tile's k-slices in slice order, the bias, and the same
 // selection as router_ring_kernel (16 tokens x 16 expert slots, E <= 16).
 __global__ __launch_bounds__(256) void router_reduce_kernel(
@@ -516,20 +686,36 @@ int launch_topk_route(const float* logits, const float* bias, int32_t* ids32, in
 }
 
 // The three bf16 planes, then (256-byte aligned) the split path's partial
-// logits [tiles][slices][16 tokens][16 experts] fp32.
+// logits [tiles][slices][16 tokens][16 experts] fp32, then for E <= 16 the
+// planes in fragment order ([ceil(H/32)][F][64 lanes][16 bytes]).
 static int64_t router_partials_offset(int64_t experts, int64_t hidden) {
     return (3 * experts * hidden * 2 + 255) & ~static_cast<int64_t>(255);
 }
 
-int64_t router_scratch_bytes(int64_t experts, int64_t hidden) {
+static int64_t router_fragments_offset(int64_t experts, int64_t hidden) {
     return router_partials_offset(experts, hidden) + kRouterPartialBytes;
+}
+
+static int64_t router_fragment_chunks(int64_t experts, int64_t hidden) {
+    return experts <= kDirectMaxExperts ? (hidden + 63) / 64 * router_fragments(static_cast<int>(experts)) * 64 : 0;
+}
+
+int64_t router_scratch_bytes(int64_t experts, int64_t hidden) {
+    return router_fragments_offset(experts, hidden) + router_fragment_chunks(experts, hidden) * 16;
 }
 
 int launch_router_split(const float* router_w, uint16_t* planes, int experts, int hidden, hipStream_t stream) {
     const int64_t n = static_cast<int64_t>(experts) * hidden;
     hipLaunchKernelGGL(router_split_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0, stream,
                        router_w, planes, n);
-    return check_launch("router_split_kernel");
+    const int rc = check_launch("router_split_kernel");
+    const int64_t chunks = router_fragment_chunks(experts, hidden);
+    if (rc != MOE_OK || chunks == 0) return rc;
+    uint16_t* frags = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(planes) +
+                                                  router_fragments_offset(experts, hidden));
+    hipLaunchKernelGGL(router_fragment_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0,
+                       stream, planes, frags, experts, hidden, chunks);
+    return check_launch("router_fragment_kernel");
 }
 
 int launch_router_fused(const uint16_t* x, const float* router_w, const float* bias,
@@ -570,8 +756,35 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
                        dim3(static_cast<unsigned>((tokens + kRouterTokens * MTV - 1) / (kRouterTokens * MTV))), \
                        dim3(256), 0, stream, x, planes, bias, ids32, ids64, weights, logits_out, tokens, \
                        hidden, experts, topk, nullptr, 1, 0)
-    // Token tiles per block: one for E <= 16 (the four waves split k), two
-    // above (the waves split the 16x16 output tiles).
+    // E <= 16 and hidden <= 8192: the VGPR-load kernel, 16 tokens per block.
+    // Otherwise the LDS ring: one token tile per block for E <= 16 (the four
+    // waves split k), two above (the waves split the 16x16 output tiles).
+    const int per = ((hidden + 63) / 64 + kDirectWaves - 1) / kDirectWaves;
+    if (experts <= kDirectMaxExperts && per <= kDirectMaxPer) {
+        const uint16_t* frags = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(planes) +
+                                                                  router_fragments_offset(experts, hidden));
+        const dim3 grid(static_cast<unsigned>((tokens + kRouterTokens - 1) / kRouterTokens));
+        const int f = router_fragments(experts);
+#define MOE_DIRECT_CASE(P, FV)                                                                              \
+    hipLaunchKernelGGL((router_direct_kernel<P, FV>), grid, dim3(kDirectWaves * 64), 0, stream, x, frags, \
+                       bias, ids32, ids64, weights, logits_out, tokens, hidden, experts, topk)
+#define MOE_DIRECT_PER(FV)                    \
+    if (per <= 2) MOE_DIRECT_CASE(2, FV);       \
+    else if (per <= 4) MOE_DIRECT_CASE(4, FV);  \
+    else if (per <= 8) MOE_DIRECT_CASE(8, FV);  \
+    else MOE_DIRECT_CASE(16, FV);
+        switch (f) {
+            case 1: MOE_DIRECT_PER(1) break;
+            case 2: MOE_DIRECT_PER(2) break;
+            case 3: MOE_DIRECT_PER(3) break;
+            case 4: MOE_DIRECT_PER(4) break;
+            case 5: MOE_DIRECT_PER(5) break;
+            default: MOE_DIRECT_PER(6) break;
+        }
+#undef MOE_DIRECT_PER
+#undef MOE_DIRECT_CASE
+        return check_launch("router_direct_kernel");
+    }
     if (experts <= 16) {
         MOE_ROUTER_CASE(1, 1);
     } else if (experts <= 32) {

@@ -71,7 +71,12 @@ def test_zero_logits_known_answer_and_empty_batch(ext):
      # Split-k routing (tokens <= 64, E <= 16, 16..256 stages of 64 hidden):
      # one token; a ragged last stage inside the last slice; the largest split
      # (16 slices of 16 stages); one stage past it (the single-workgroup path).
-     (1, 4096, 8, 2), (16, 4096, 16, 6), (33, 2040, 12, 3), (50, 16384, 4, 2), (3, 16448, 8, 2)],
+     (1, 4096, 8, 2), (16, 4096, 16, 6), (33, 2040, 12, 3), (50, 16384, 4, 2), (3, 16448, 8, 2),
+     # E <= 16 past the split sizes: the VGPR-load kernel with 1 to 6 weight fragments
+     # (E = 2, 3, 8, 10, 12, 16) and 2, 8 and 16 steps of 64 hidden per wave (ragged
+     # last token tile, k tail inside a step); hidden 8200 takes the ring.
+     (300, 4096, 8, 2), (1000, 8192, 16, 2), (77, 200, 3, 2), (130, 8200, 8, 2), (90, 256, 2, 1),
+     (65, 320, 10, 3), (70, 64, 12, 4)],
 )
 def test_fused_router_matches_oracle(ext, tokens, hidden, experts, topk):
     generator = torch.Generator(device="cuda").manual_seed(tokens + hidden)
