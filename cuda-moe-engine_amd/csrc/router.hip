@@ -460,8 +460,10 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
 // its own accumulator; per token and plane row the block sums the halves and
 // the waves in order, and the logit is (lo + mid) + hi.
 //
-// A block owns 16 tokens (two groups of 8); its eight waves split the 64-k
-// steps into eight contiguous ranges of at most PER. The range is unrolled at
+// A block owns 16 tokens (two groups of 8); its two waves split the 64-k
+// steps into two contiguous ranges of at most PER (at H=4096, 4096 tokens:
+// 7.7, 7.3 and 7.3 us with eight, four and two waves; fewer partials to add,
+// longer load streams per wave; 8.5 us with sixteen). The range is unrolled at
 // compile time with the loads D steps ahead of the multiplies, so the code is
 // straight-line and the compiler's wait before each multiply counts only the
 // loads issued after that step's (a runtime loop carried the in-flight
@@ -474,8 +476,8 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
 // the zero rows of unused expert slots), and at H=4096, 4096 tokens its time
 // did not move when either the x or the plane loads were replaced by
 // out-of-range (zero, no traffic) ones: 12.3 us.
-constexpr int kDirectWaves = 8;
-constexpr int kDirectMaxPer = 16;   // 64-k steps per wave: hidden <= 8 * 16 * 64 = 8192
+constexpr int kDirectWaves = 2;
+constexpr int kDirectMaxPer = 64;   // 64-k steps per wave: hidden <= 2 * 64 * 64 = 8192
 constexpr int kDirectMaxExperts = 16;
 
 __host__ __device__ constexpr int router_fragments(int experts) { return (6 * experts + 15) / 16; }
@@ -772,7 +774,9 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
     if (per <= 2) MOE_DIRECT_CASE(2, FV);       \
     else if (per <= 4) MOE_DIRECT_CASE(4, FV);  \
     else if (per <= 8) MOE_DIRECT_CASE(8, FV);  \
-    else MOE_DIRECT_CASE(16, FV);
+    else if (per <= 16) MOE_DIRECT_CASE(16, FV);  \
+    else if (per <= 32) MOE_DIRECT_CASE(32, FV);  \
+    else MOE_DIRECT_CASE(64, FV);
         switch (f) {
             case 1: MOE_DIRECT_PER(1) break;
             case 2: MOE_DIRECT_PER(2) break;
