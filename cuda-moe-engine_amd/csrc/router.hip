@@ -519,6 +519,7 @@ __global__ __launch_bounds__(kDirectWaves * 64) void router_direct_kernel(
     float* __restrict__ logits_out, int64_t tokens, int hidden, int experts, int topk) {
     constexpr int TB = kRouterTokens, PR = 8 * F, PRP = 2 * PR + 1;
     constexpr int D = direct_depth<PER, F>();
+    static_assert(kDirectWaves * 8 >= TB, "the selection takes eight lanes per token");
     __shared__ float part[kDirectWaves][TB][PRP];  // [wave][token][half * PR + plane row]
     __shared__ float sbias[kDirectMaxExperts];
     const int lane = threadIdx.x & 63;
