@@ -104,26 +104,59 @@ def time_loop(fn, steps, warmup):
     return s.elapsed_time(e) * 1000.0 / steps
 
 
+def time_graph(fn, reps, warmup):
+    """Mean GPU time of one fn() call: `reps` back-to-back calls captured in a
+    HIP graph and replayed (no host launch overhead in the measurement)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(reps):
+                fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) * 1000.0 / reps
+
+
 def time_stages(block, x, steps, warmup):
-    """Per-stage mean latency: each stage repeated back to back on its own inputs
+    """Per-stage GPU time: the forward's own C-ABI calls (the block's pre-bound
+    launches, router split already done), each repeated back to back in a graph
     (every stage is idempotent given the previous stage's outputs)."""
     import torch
 
-    state = block.workspace(x)
-    ext = block._extension
+    from moe_dispatch._extension import current_stream_handle
+
     with torch.inference_mode():
-        ids32, ids64, weights = block.route(x)
-        state.transport.dispatch(x, ids32, ids64)
+        block(x)  # a validated forward binds the launches; the next ones reuse them
+        launches = block._launches[(x.shape[0], x.device)]
+        assert launches.still_valid(block)
+        lib, bound, x_ptr = launches.lib, launches, x.data_ptr()
+
+        def call(name, *args):
+            lib.check(getattr(lib, name)(*args, current_stream_handle(bound.device_index)), name)
+
+        router_fn = "moe_router_fused_ranked" if bound.ranked else "moe_router_fused"
+        dispatch_fn = "moe_dispatch_ranked" if bound.ranked else "moe_dispatch"
         stages = {
-            "router": lambda: block.route(x),
-            "dispatch": lambda: state.transport.dispatch(x, ids32, ids64),
-            "gateup_swiglu": lambda: ext.gateup_swiglu_out(state.transport.packed, block.gate_up_weight,
-                                                           state.transport.offsets, state.activated),
-            "down": lambda: ext.grouped_gemm_out(state.activated, block.down_weight, state.transport.offsets,
-                                                 state.expert_output),
-            "combine": lambda: state.transport.combine(state.expert_output, weights),
+            "router": lambda: call(router_fn, x_ptr, None, *bound.router),
+            "dispatch": lambda: call(dispatch_fn, x_ptr, *bound.dispatch),
+            "gateup_swiglu": lambda: call("moe_grouped_gateup_swiglu", *bound.gateup),
+            "down": lambda: call("moe_grouped_gemm", *bound.down),
+            "combine": lambda: call("moe_combine", *bound.combine),
         }
-        return {name: {"mean_us": time_loop(fn, steps, warmup)} for name, fn in stages.items()}
+        return {name: {"mean_us": time_graph(fn, steps, warmup)} for name, fn in stages.items()}
 
 
 def _cpu_model():
@@ -336,21 +369,13 @@ def transport_bench(args):
     y = torch.randn(ws.capacity_rows, hidden, device="cuda",
                     generator=torch.Generator(device="cuda").manual_seed(1)).bfloat16()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # GPU time per call: back-to-back calls replayed from a HIP graph (the host
+    # work of a Python call is about as long as these kernels).
     with torch.inference_mode():
-        for _ in range(args.warmup):
-            ws.dispatch(x, ids32, ids64)
-            ws.combine(y, weights)
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(args.steps):
-            ws.dispatch(x, ids32, ids64)
-            ws.combine(y, weights)
-        end.record()
-        torch.cuda.synchronize()
-        d_us = time_loop(lambda: ws.dispatch(x, ids32, ids64), args.steps, args.warmup)
-        c_us = time_loop(lambda: ws.combine(y, weights), args.steps, args.warmup)
-    mean_us = start.elapsed_time(end) * 1000.0 / args.steps
+        mean_us = time_graph(lambda: (ws.dispatch(x, ids32, ids64), ws.combine(y, weights)), args.steps,
+                             max(args.warmup, 1))
+        d_us = time_graph(lambda: ws.dispatch(x, ids32, ids64), args.steps, max(args.warmup, 1))
+        c_us = time_graph(lambda: ws.combine(y, weights), args.steps, max(args.warmup, 1))
     pad_rows = int(ws.offsets[-1].item()) - tokens * topk
     disp_bytes = dispatch_bytes(tokens, hidden, topk, pad_rows)
     comb_bytes = combine_bytes(tokens, hidden, topk)

@@ -13,12 +13,16 @@ namespace moe {
 int launch_topk_route(const float*, const float*, int32_t*, int64_t*, float*, int64_t, int, int,
                       hipStream_t);
 int launch_router_fused(const uint16_t*, const float*, const float*, int32_t*, int64_t*, float*,
-                        float*, uint16_t*, int64_t, int, int, int, hipStream_t);
+                        float*, uint16_t*, int64_t, int, int, int, int32_t*, int32_t*, hipStream_t);
+int64_t router_rank_tile(int64_t, int64_t);
 int launch_router_split(const float*, uint16_t*, int, int, hipStream_t);
 int64_t router_scratch_bytes(int64_t, int64_t);
 int64_t dispatch_scratch_bytes(int64_t, int64_t, int64_t);
 int launch_dispatch(const void*, int, const int32_t*, int32_t*, int32_t*, int32_t*, void*,
-                    int32_t*, int32_t*, int64_t, int64_t, int, int, int, bool, hipStream_t);
+                    int32_t*, int32_t*, int64_t, int64_t, int, int, int, int64_t, bool, hipStream_t);
+int launch_dispatch_ranked(const void*, int, const int32_t*, int32_t*, int32_t*, int32_t*, void*, int32_t*,
+                           const int32_t*, const int32_t*, int64_t, int64_t, int64_t, int, int, int, int64_t, bool,
+                           hipStream_t);
 int launch_combine(const void*, int, const int32_t*, const float*, void*, int64_t, int64_t, int,
                    int64_t, hipStream_t);
 int launch_swiglu(const void*, int, const int32_t*, void*, int64_t, int64_t, hipStream_t);
@@ -110,10 +114,11 @@ int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden) {
     return router_scratch_bytes(experts, hidden);
 }
 
-int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
-                     int64_t* ids64, float* weights, float* logits_out, void* scratch,
-                     int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
-                     int64_t topk, void* stream) {
+// The fused router's checks (both entry points); MOE_OK when it may launch.
+static int check_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
+                              int64_t* ids64, float* weights, float* logits_out, void* scratch,
+                              int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                              int64_t topk) {
     MOE_REQUIRE(tokens >= 0, MOE_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
     MOE_REQUIRE(hidden >= 8 && hidden % 8 == 0 && hidden <= INT_MAX, MOE_ERR_UNSUPPORTED,
                 "fused router needs hidden a positive multiple of 8");
@@ -134,9 +139,48 @@ int moe_router_fused(const void* x, const float* router_w, const float* bias, in
     MOE_REQUIRE(aligned_to(bias, 4) && aligned_to(ids32, 4) && aligned_to(weights, 4) &&
                     aligned_to(logits_out, 4) && aligned_to(ids64, 8),
                 MOE_ERR_INVALID_ARGUMENT, "pointers must be aligned to their element size");
+    return MOE_OK;
+}
+
+int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
+                     int64_t* ids64, float* weights, float* logits_out, void* scratch,
+                     int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                     int64_t topk, void* stream) {
+    const int rc = check_router_fused(x, router_w, bias, ids32, ids64, weights, logits_out, scratch,
+                                      scratch_bytes, tokens, hidden, experts, topk);
+    if (rc != MOE_OK || tokens == 0) return rc;
     return launch_router_fused(static_cast<const uint16_t*>(x), router_w, bias, ids32, ids64,
                                weights, logits_out, static_cast<uint16_t*>(scratch), tokens,
-                               (int)hidden, (int)experts, (int)topk, static_cast<hipStream_t>(stream));
+                               (int)hidden, (int)experts, (int)topk, nullptr, nullptr,
+                               static_cast<hipStream_t>(stream));
+}
+
+int64_t moe_router_rank_tile(int64_t tokens, int64_t experts) {
+    if (tokens < 0 || experts < 1 || experts > kMaxExperts) return -1;
+    return router_rank_tile(tokens, experts);
+}
+
+int moe_router_fused_ranked(const void* x, const float* router_w, const float* bias, int32_t* ids32,
+                            int64_t* ids64, float* weights, float* logits_out, void* scratch,
+                            int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                            int64_t topk, int32_t* ranks, int32_t* tile_counts, int64_t tile_counts_bytes,
+                            void* stream) {
+    const int rc = check_router_fused(x, router_w, bias, ids32, ids64, weights, logits_out, scratch,
+                                      scratch_bytes, tokens, hidden, experts, topk);
+    if (rc != MOE_OK || tokens == 0) return rc;
+    const int64_t tile = router_rank_tile(tokens, experts);
+    MOE_REQUIRE(tile > 0, MOE_ERR_UNSUPPORTED,
+                "ranked routing needs ceil(tokens/tile) * experts <= 4096 (moe_router_rank_tile returned 0)");
+    const int64_t need = (tokens + tile - 1) / tile * experts * 4;
+    MOE_REQUIRE(tile_counts_bytes >= need, MOE_ERR_WORKSPACE, "tile counts need %lld bytes, got %lld",
+                (long long)need, (long long)tile_counts_bytes);
+    MOE_REQUIRE(ranks && tile_counts, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(aligned_to(ranks, 4) && aligned_to(tile_counts, 4), MOE_ERR_INVALID_ARGUMENT,
+                "index buffers must be 4-byte aligned");
+    return launch_router_fused(static_cast<const uint16_t*>(x), router_w, bias, ids32, ids64,
+                               weights, logits_out, static_cast<uint16_t*>(scratch), tokens,
+                               (int)hidden, (int)experts, (int)topk, ranks, tile_counts,
+                               static_cast<hipStream_t>(stream));
 }
 
 int moe_router_split(const float* router_w, void* scratch, int64_t scratch_bytes, int64_t experts,
@@ -160,11 +204,10 @@ int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk
     return dispatch_scratch_bytes(tokens, experts, topk);
 }
 
-int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
-                 int32_t* slots, void* packed, int32_t* inverse, void* scratch,
-                 int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
-                 int64_t topk, int64_t alignment, int64_t packed_rows, int vectorized,
-                 void* stream) {
+// The dispatch checks shared by moe_dispatch and moe_dispatch_ranked (all but the scratch).
+static int check_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                          int32_t* slots, void* packed, int32_t* inverse, int64_t tokens, int64_t hidden,
+                          int64_t experts, int64_t topk, int64_t alignment, int64_t packed_rows) {
     MOE_REQUIRE(valid_dtype(dtype), MOE_ERR_INVALID_ARGUMENT, "only FP32, FP16 and BF16 are supported");
     MOE_REQUIRE(tokens >= 0 && hidden > 0, MOE_ERR_INVALID_ARGUMENT, "incompatible token dimensions");
     MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
@@ -177,23 +220,72 @@ int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, 
     MOE_REQUIRE(packed_rows >= required, MOE_ERR_WORKSPACE,
                 "packed workspace has %lld rows, needs %lld", (long long)packed_rows,
                 (long long)required);
-    const int64_t need = dispatch_scratch_bytes(tokens, experts, topk);
-    MOE_REQUIRE(scratch_bytes >= need, MOE_ERR_WORKSPACE, "dispatch scratch has %lld bytes, needs %lld",
-                (long long)scratch_bytes, (long long)need);
-    MOE_REQUIRE(counts && offsets && scratch, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(counts && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
     MOE_REQUIRE(n == 0 || (x && ids && slots && packed && inverse), MOE_ERR_INVALID_ARGUMENT,
                 "null pointer");
+    return MOE_OK;
+}
+
+static int check_dispatch_alignment(const void* x, int dtype, void* packed, const int32_t* ids, int32_t* counts,
+                                    int32_t* offsets, int32_t* slots, int32_t* inverse, const void* table) {
     // Rows are copied with the widest access that the row size and both base
     // addresses allow (launch_dispatch), down to one element.
     const uintptr_t elem = static_cast<uintptr_t>(dtype_size(dtype));
     MOE_REQUIRE(aligned_to(x, elem) && aligned_to(packed, elem), MOE_ERR_INVALID_ARGUMENT,
                 "x and packed must be aligned to their element size");
     MOE_REQUIRE(aligned_to(ids, 4) && aligned_to(counts, 4) && aligned_to(offsets, 4) &&
-                    aligned_to(slots, 4) && aligned_to(inverse, 4) && aligned_to(scratch, 4),
+                    aligned_to(slots, 4) && aligned_to(inverse, 4) && aligned_to(table, 4),
                 MOE_ERR_INVALID_ARGUMENT, "index buffers must be 4-byte aligned");
+    return MOE_OK;
+}
+
+int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                 int32_t* slots, void* packed, int32_t* inverse, void* scratch,
+                 int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                 int64_t topk, int64_t alignment, int64_t packed_rows, int vectorized,
+                 void* stream) {
+    const int rc = check_dispatch(x, dtype, ids, counts, offsets, slots, packed, inverse, tokens, hidden,
+                                  experts, topk, alignment, packed_rows);
+    if (rc != MOE_OK) return rc;
+    const int64_t need = dispatch_scratch_bytes(tokens, experts, topk);
+    MOE_REQUIRE(scratch_bytes >= need, MOE_ERR_WORKSPACE, "dispatch scratch has %lld bytes, needs %lld",
+                (long long)scratch_bytes, (long long)need);
+    MOE_REQUIRE(scratch, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    const int ra = check_dispatch_alignment(x, dtype, packed, ids, counts, offsets, slots, inverse, scratch);
+    if (ra != MOE_OK) return ra;
     return launch_dispatch(x, dtype, ids, counts, offsets, slots, packed, inverse,
                            static_cast<int32_t*>(scratch), tokens, hidden, (int)experts, (int)topk,
-                           (int)alignment, vectorized != 0, static_cast<hipStream_t>(stream));
+                           (int)alignment, packed_rows, vectorized != 0, static_cast<hipStream_t>(stream));
+}
+
+int moe_dispatch_ranked(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                        int32_t* slots, void* packed, int32_t* inverse, const int32_t* ranks,
+                        const int32_t* tile_counts, int64_t tile_counts_bytes, int64_t tile_tokens, int64_t tokens,
+                        int64_t hidden, int64_t experts, int64_t topk, int64_t alignment, int64_t packed_rows,
+                        int vectorized, void* stream) {
+    const int rc = check_dispatch(x, dtype, ids, counts, offsets, slots, packed, inverse, tokens, hidden,
+                                  experts, topk, alignment, packed_rows);
+    if (rc != MOE_OK) return rc;
+    const int64_t tile = router_rank_tile(tokens, experts);
+    MOE_REQUIRE(tokens == 0 || (tile > 0 && tile_tokens == tile), MOE_ERR_INVALID_ARGUMENT,
+                "tile_tokens %lld is not the ranked route's tile (%lld) for this shape", (long long)tile_tokens,
+                (long long)tile);
+    if (tokens > 0) {
+        const int64_t need = (tokens + tile - 1) / tile * experts * 4;
+        MOE_REQUIRE(tile_counts_bytes >= need, MOE_ERR_WORKSPACE, "tile counts need %lld bytes, got %lld",
+                    (long long)need, (long long)tile_counts_bytes);
+        MOE_REQUIRE(ranks && tile_counts, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    }
+    int ra = check_dispatch_alignment(x, dtype, packed, ids, counts, offsets, slots, inverse, tile_counts);
+    if (ra != MOE_OK) return ra;
+    MOE_REQUIRE(aligned_to(ranks, 4), MOE_ERR_INVALID_ARGUMENT, "index buffers must be 4-byte aligned");
+    if (tokens == 0)  // no assignments: counts and offsets are zero (no tile table is read)
+        return launch_dispatch(x, dtype, ids, counts, offsets, slots, packed, inverse, nullptr, tokens, hidden,
+                               (int)experts, (int)topk, (int)alignment, packed_rows, vectorized != 0,
+                               static_cast<hipStream_t>(stream));
+    return launch_dispatch_ranked(x, dtype, ids, counts, offsets, slots, packed, inverse, ranks, tile_counts,
+                                  tile, tokens, hidden, (int)experts, (int)topk, (int)alignment, packed_rows,
+                                  vectorized != 0, static_cast<hipStream_t>(stream));
 }
 
 int moe_combine(const void* expert_output, int dtype, const int32_t* inverse,

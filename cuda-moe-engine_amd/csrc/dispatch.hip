@@ -114,13 +114,17 @@ template <> __device__ __forceinline__ uint16_t zero_vec<uint16_t>() { return 0;
 // two-kernel path's.
 constexpr int kSmallAssign = 1024;
 
+// Ranks (in-chunk, !COUNT) come from `ranks`: the count/rank pass writes them
+// into slots itself, a ranked route into a buffer of its own. Destination and
+// padding rows are kept below packed_rows (they are for consistent counts and
+// ranks; a caller's inconsistent pair is not written out of bounds).
 template <int VB, bool COUNT>
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(
-    const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* __restrict__ slots,
-    const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
+    const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* slots,
+    const int32_t* ranks, const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
     int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
-    int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2) {
+    int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2, int64_t packed_rows) {
     using V = typename VecOf<VB>::T;
     __shared__ int part_all[kPackThreads / kWave][kMaxExperts];
     __shared__ int part_before[kPackThreads / kWave][kMaxExperts];
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int my_e = tid < n_local ? ids[my_p] : -1;
     int my_rank = -1;
     if constexpr (!COUNT) {
-        if (tid < n_local) my_rank = slots[my_p];
+        if (tid < n_local) my_rank = ranks[my_p];
     }
 
     if constexpr (COUNT) {
@@ -208,14 +212,26 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     } else {
     // (a) Column sums of chunk_counts: all chunks, and chunks before mine.
     //     Thread tid always sees expert tid % experts_pow2 (a divisor of 256).
+    //     Loads go out eight at a time (independent), not one per loop trip:
+    //     the table has up to 4096 entries (16 per thread) and each trip's L2
+    //     latency would otherwise add up on every block's critical path.
     {
         const int e = tid % experts_pow2;
+        const int stride = kPackThreads / experts_pow2;
         int s_all = 0, s_before = 0;
         if (e < experts) {
-            for (int c = tid / experts_pow2; c < n_chunks; c += kPackThreads / experts_pow2) {
-                const int v = chunk_counts[static_cast<int64_t>(c) * experts + e];
-                s_all += v;
-                if (c < my_chunk) s_before += v;
+            for (int c0 = tid / experts_pow2; c0 < n_chunks; c0 += 8 * stride) {
+                int v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int c = c0 + j * stride;
+                    v[j] = c < n_chunks ? chunk_counts[static_cast<int64_t>(c) * experts + e] : 0;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    s_all += v[j];
+                    if (c0 + j * stride < my_chunk) s_before += v[j];
+                }
             }
         }
         for (int m = experts_pow2; m < kWave; m <<= 1) {
@@ -266,14 +282,15 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
         int64_t d = -1;
         if (e >= 0 && e < experts) {
             const int r = COUNT ? own_rank[tid] : my_rank;
-            if (r >= 0) {
-                const int slot = before[e] + r;
-                d = static_cast<int64_t>(offs[e]) + slot;
-                slots[my_p] = slot;
+            const int64_t slot = static_cast<int64_t>(before[e]) + r;
+            const int64_t row = static_cast<int64_t>(offs[e]) + slot;
+            if (r >= 0 && slot >= 0 && row >= 0 && row < packed_rows) {
+                d = row;
+                slots[my_p] = static_cast<int32_t>(slot);
                 inverse[my_p] = static_cast<int32_t>(d);
             }
-        } else if constexpr (COUNT) {
-            slots[my_p] = -1;  // (count_rank_kernel writes this on the other path)
+        } else {
+            slots[my_p] = -1;  // out-of-range id (the count/rank pass also writes -1)
         }
         dest[tid] = d;
     }
@@ -297,8 +314,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
 
     // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
     for (int e = blockIdx.x; e < experts; e += gridDim.x) {
-        const int64_t r0 = offs[e] + total[e];
-        const int64_t r1 = offs[e + 1];
+        const int64_t r0 = max(static_cast<int64_t>(offs[e]) + total[e], static_cast<int64_t>(0));
+        const int64_t r1 = min(static_cast<int64_t>(offs[e + 1]), packed_rows);
         const int64_t pad_items = (r1 - r0) * nv;
         V* base = reinterpret_cast<V*>(packed + r0 * row_bytes);
         for (int64_t i = tid; i < pad_items; i += kPackThreads) base[i] = zero_vec<V>();
@@ -420,11 +437,14 @@ static int64_t pow2_at_least(int64_t v) {
 }
 
 // Chunk size keeps n_chunks * E <= kPrefixMax (each pack block rebuilds its
-// prefix from the whole chunk_counts table); pack blocks move about 16 KiB of rows.
-static DispatchPlan plan_dispatch(int64_t tokens, int64_t experts, int64_t topk, int64_t row_bytes) {
+// prefix from the whole chunk_counts table) unless the chunks are given (the
+// router's tiles); pack blocks move about 16 KiB of rows.
+static DispatchPlan plan_dispatch(int64_t tokens, int64_t experts, int64_t topk, int64_t row_bytes,
+                                  int64_t given_chunk = 0) {
     DispatchPlan p{};
     int64_t chunk = 16;
     while (chunk < tokens && ((tokens + chunk - 1) / chunk) * experts > kPrefixMax) chunk <<= 1;
+    if (given_chunk > 0) chunk = given_chunk;
     p.chunk_tokens = chunk;
     p.n_chunks = tokens > 0 ? (tokens + chunk - 1) / chunk : 0;
     int64_t pt = 1;
@@ -446,15 +466,53 @@ int64_t dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk) {
     return (n > 0 ? n : 1) * static_cast<int64_t>(sizeof(int32_t));
 }
 
+static int launch_pack(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                       int32_t* slots, const int32_t* ranks, void* packed, int32_t* inverse,
+                       const int32_t* chunk_counts, int64_t tokens, int64_t hidden, int experts, int topk,
+                       int alignment, int64_t packed_rows, bool vectorized, const DispatchPlan& plan,
+                       bool count_in_pack, hipStream_t stream);
+
 int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts,
                     int32_t* offsets, int32_t* slots, void* packed, int32_t* inverse,
                     int32_t* chunk_counts, int64_t tokens, int64_t hidden, int experts, int topk,
-                    int alignment, bool vectorized, hipStream_t stream) {
-    const int64_t elem = dtype_size(dtype);
-    const int64_t row_bytes = hidden * elem;
+                    int alignment, int64_t packed_rows, bool vectorized, hipStream_t stream) {
+    const int64_t row_bytes = hidden * dtype_size(dtype);
     const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes);
     const int64_t n_assign = tokens * topk;
     const bool count_in_pack = n_assign <= kSmallAssign;
+    if (plan.n_chunks > 0 && !count_in_pack) {
+        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)),
+                           dim3(kRankThreads), 0, stream, ids, slots, chunk_counts, n_assign,
+                           experts, plan.chunk_tokens * topk);
+        int rc = check_launch("count_rank_kernel");
+        if (rc != MOE_OK) return rc;
+    }
+    return launch_pack(x, dtype, ids, counts, offsets, slots, slots, packed, inverse, chunk_counts, tokens,
+                       hidden, experts, topk, alignment, packed_rows, vectorized, plan, count_in_pack, stream);
+}
+
+// Dispatch after a ranked route: `ranks` holds the in-tile ranks and
+// tile_counts the per-tile counts of tiles of tile_tokens tokens (the
+// count/rank pass's formats, with the tiles as chunks), so only the pack
+// kernel runs. It does not write `ranks`, so it can run again on them.
+int launch_dispatch_ranked(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                           int32_t* slots, void* packed, int32_t* inverse, const int32_t* ranks,
+                           const int32_t* tile_counts, int64_t tile_tokens, int64_t tokens, int64_t hidden,
+                           int experts, int topk, int alignment, int64_t packed_rows, bool vectorized,
+                           hipStream_t stream) {
+    const int64_t row_bytes = hidden * dtype_size(dtype);
+    const DispatchPlan plan = plan_dispatch(tokens, experts, topk, row_bytes, tile_tokens);
+    return launch_pack(x, dtype, ids, counts, offsets, slots, ranks, packed, inverse, tile_counts, tokens,
+                       hidden, experts, topk, alignment, packed_rows, vectorized, plan, false, stream);
+}
+
+static int launch_pack(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                       int32_t* slots, const int32_t* ranks, void* packed, int32_t* inverse,
+                       const int32_t* chunk_counts, int64_t tokens, int64_t hidden, int experts, int topk,
+                       int alignment, int64_t packed_rows, bool vectorized, const DispatchPlan& plan,
+                       bool count_in_pack, hipStream_t stream) {
+    const int64_t elem = dtype_size(dtype);
+    const int64_t row_bytes = hidden * elem;
     // The widest access that divides the row size and both base addresses (an
     // offset view of a larger tensor may start at any element).
     int vb = static_cast<int>(elem);
@@ -470,21 +528,14 @@ int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* count
     }
     MOE_REQUIRE(plan.pack_tokens * (row_bytes / vb) <= INT32_MAX, MOE_ERR_UNSUPPORTED,
                 "row of %lld bytes too large for the pack kernel", (long long)row_bytes);
-    if (plan.n_chunks > 0 && !count_in_pack) {
-        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)),
-                           dim3(kRankThreads), 0, stream, ids, slots, chunk_counts, n_assign,
-                           experts, plan.chunk_tokens * topk);
-        int rc = check_launch("count_rank_kernel");
-        if (rc != MOE_OK) return rc;
-    }
     const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
     const dim3 grid(static_cast<unsigned>(plan.pack_blocks));
 #define MOE_PACK_LAUNCH(VBV, CNT)                                                              \
     hipLaunchKernelGGL((pack_kernel<VBV, CNT>), grid, dim3(kPackThreads), 0, stream,            \
-                       static_cast<const char*>(x), ids, slots, chunk_counts, counts, offsets,   \
+                       static_cast<const char*>(x), ids, slots, ranks, chunk_counts, counts, offsets, \
                        static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,    \
                        alignment, plan.chunk_tokens, plan.pack_tokens,                          \
-                       static_cast<int>(plan.n_chunks), experts_pow2)
+                       static_cast<int>(plan.n_chunks), experts_pow2, packed_rows)
 #define MOE_PACK_CASE(VBV)                 \
     if (count_in_pack)                     \
         MOE_PACK_LAUNCH(VBV, true);        \

@@ -116,6 +116,7 @@ __global__ __launch_bounds__(256) void topk_route_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 
 constexpr int kRouterTokens = 16;
+constexpr int64_t kRankedPrefixMax = 4096;  // routing tiles x experts of a ranked route
 constexpr int kRouterSplitTokens = 64;  // split-k routing up to this many tokens (E <= 16)
 constexpr int kRouterSplitSlices = 16;
 constexpr int kRouterSplitTiles = kRouterSplitTokens / kRouterTokens;
@@ -178,7 +179,8 @@ __global__ __launch_bounds__(256) void router_split_kernel(const float* __restri
 // reference's iterative argmax with ties to the lower id. Lane 0 writes.
 template <int EPL>
 __device__ __forceinline__ void select_eight_lanes(float (&v)[EPL], int sub, int topk, int64_t token,
-                                                   int32_t* ids32, int64_t* ids64, float* weights) {
+                                                   int32_t* ids32, int64_t* ids64, float* weights,
+                                                   int* tile_ids = nullptr) {
     float sel_v[kMaxTopk];
     int sel_i[kMaxTopk];
 #pragma unroll
@@ -206,7 +208,50 @@ __device__ __forceinline__ void select_eight_lanes(float (&v)[EPL], int sub, int
             for (int j = 0; j < EPL; ++j) v[j] = (sub * EPL + j == bi) ? -INFINITY : v[j];
         }
     }
-    if (sub == 0) write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
+    if (sub == 0) {
+        write_route(sel_v, sel_i, topk, token, ids32, ids64, weights);
+        if (tile_ids) {
+#pragma unroll
+            for (int k = 0; k < kMaxTopk; ++k)
+                if (k < topk) tile_ids[k] = sel_i[k];
+        }
+    }
+}
+
+// In-tile ranks and counts for the dispatch (the work of its count/rank pass,
+// done here while the ids are at hand). The block's tile holds tokens t0 ..
+// t0 + n_tok - 1; their n = n_tok * K selected ids sit in tile_ids (LDS, flat
+// order). One wave walks them in rounds of 64: lanes holding the same id are
+// found by intersecting six bit-plane ballots, and a lane's rank is the number
+// of such lanes below it plus its expert's count from earlier rounds, which
+// lane e keeps in a register (read with a cross-lane shuffle; one ballot per
+// expert adds each round's counts). ranks[p] <- rank of assignment p among
+// the tile's earlier assignments to the same expert; counts_row[e] <- the
+// tile's assignments to expert e.
+__device__ __forceinline__ void rank_tile(const int* tile_ids, int n, int64_t p0, int experts, int32_t* ranks,
+                                          int32_t* counts_row) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t lanes_below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    int run = 0;  // lane e < experts: the tile's assignments to expert e so far
+    for (int base = 0; base < n; base += kWave) {
+        const int i = base + lane;
+        const bool valid = i < n;
+        const int e = valid ? tile_ids[i] : 0;
+        uint64_t same = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 6; ++b) {
+            const bool bit = (e >> b) & 1;
+            const uint64_t plane = __ballot(valid && bit);
+            same &= bit ? plane : ~plane;
+        }
+        const int prior = __shfl(run, e);
+        if (valid) ranks[p0 + i] = prior + __popcll(same & lanes_below);
+        for (int x = 0; x < experts; ++x) {
+            const int c = __popcll(__ballot(valid && e == x));
+            if (lane == x) run += c;
+        }
+    }
+    if (lane < experts) counts_row[lane] = run;
 }
 
 typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
@@ -253,7 +298,8 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ planes,
     const float* __restrict__ bias, int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
     float* __restrict__ weights, float* __restrict__ logits_out, int64_t tokens, int hidden,
-    int experts, int topk, float* __restrict__ partials, int slices, int per) {
+    int experts, int topk, float* __restrict__ partials, int slices, int per, int32_t* __restrict__ ranks,
+    int32_t* __restrict__ tile_counts) {
     using S = RouterShape<NT, MT>;
     constexpr int TB = S::TB, EB = S::EB, EBP = S::EBP, TPW = S::TPW, G = S::G, LPW = S::LPW;
     constexpr uint32_t A_STAGE = S::A_STAGE, B_STAGE = S::B_STAGE;
@@ -421,6 +467,7 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
 
     constexpr int EPL = EB / 8;
     static_assert(EPL >= 1 && TB <= 32, "eight lanes per token, at most 32 tokens per block");
+    __shared__ int tile_ids[TB * kMaxTopk];
     const int tl = wave * 8 + (lane >> 3);
     const int sub = lane & 7;
     const int64_t token = t0 + tl;
@@ -438,7 +485,13 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
                 v[j] = logit + sbias[e];
             }
         }
-        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights);
+        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights, ranks ? tile_ids + tl * topk : nullptr);
+    }
+    if (ranks) {
+        __syncthreads();
+        if (threadIdx.x < kWave)
+            rank_tile(tile_ids, static_cast<int>(rows) * topk, t0 * topk, experts, ranks,
+                      tile_counts + static_cast<int64_t>(tile) * experts);
     }
 }
 
@@ -516,12 +569,14 @@ template <int PER, int F>
 __global__ __launch_bounds__(kDirectWaves * 64) void router_direct_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ frags, const float* __restrict__ bias,
     int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, float* __restrict__ weights,
-    float* __restrict__ logits_out, int64_t tokens, int hidden, int experts, int topk) {
+    float* __restrict__ logits_out, int64_t tokens, int hidden, int experts, int topk, int32_t* __restrict__ ranks,
+    int32_t* __restrict__ tile_counts) {
     constexpr int TB = kRouterTokens, PR = 8 * F, PRP = 2 * PR + 1;
     constexpr int D = direct_depth<PER, F>();
     static_assert(kDirectWaves * 8 >= TB, "the selection takes eight lanes per token");
     __shared__ float part[kDirectWaves][TB][PRP];  // [wave][token][half * PR + plane row]
     __shared__ float sbias[kDirectMaxExperts];
+    __shared__ int tile_ids[TB * kMaxTopk];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TB;
@@ -611,7 +666,13 @@ __global__ __launch_bounds__(kDirectWaves * 64) void router_direct_kernel(
                 v[j] = logit + sbias[e];
             }
         }
-        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights);
+        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights, ranks ? tile_ids + tl * topk : nullptr);
+    }
+    if (ranks) {
+        __syncthreads();
+        if (threadIdx.x < kWave)
+            rank_tile(tile_ids, static_cast<int>(rows) * topk, t0 * topk, experts, ranks,
+                      tile_counts + static_cast<int64_t>(blockIdx.x) * experts);
     }
 }
 
@@ -620,10 +681,12 @@ __global__ __launch_bounds__(kDirectWaves * 64) void router_direct_kernel(
 __global__ __launch_bounds__(256) void router_reduce_kernel(
     const float* __restrict__ partials, const float* __restrict__ bias, int32_t* __restrict__ ids32,
     int64_t* __restrict__ ids64, float* __restrict__ weights, float* __restrict__ logits_out,
-    int64_t tokens, int experts, int topk, int slices) {
+    int64_t tokens, int experts, int topk, int slices, int32_t* __restrict__ ranks,
+    int32_t* __restrict__ tile_counts) {
     constexpr int TB = kRouterTokens, EB = 16, EPL = EB / 8;
     static_assert(TB * EB == 256, "one thread per (token, expert)");
     __shared__ float lg[TB][EB + 1];
+    __shared__ int tile_ids[TB * kMaxTopk];
     const int tile = blockIdx.x;
     {
         const int tl = threadIdx.x / EB, e = threadIdx.x % EB;
@@ -649,7 +712,15 @@ __global__ __launch_bounds__(256) void router_reduce_kernel(
                 v[j] = logit + bias[e];
             }
         }
-        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights);
+        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights, ranks ? tile_ids + tl * topk : nullptr);
+    }
+    if (ranks) {
+        __syncthreads();
+        const int64_t t0 = static_cast<int64_t>(tile) * TB;
+        const int n_tok = static_cast<int>(min(static_cast<int64_t>(TB), tokens - t0));
+        if (threadIdx.x < kWave)
+            rank_tile(tile_ids, n_tok * topk, t0 * topk, experts, ranks,
+                      tile_counts + static_cast<int64_t>(tile) * experts);
     }
 }
 
@@ -721,10 +792,20 @@ int launch_router_split(const float* router_w, uint16_t* planes, int experts, in
     return check_launch("router_fragment_kernel");
 }
 
+// Tokens per routing block: the tile whose in-tile ranks and counts the
+// ranked router writes (16 for E <= 16, 32 above), or 0 when the tile table
+// (tiles x E entries, which every pack block sums) would exceed
+// kRankedPrefixMax or there are no tokens.
+int64_t router_rank_tile(int64_t tokens, int64_t experts) {
+    const int64_t tile = experts <= 16 ? kRouterTokens : 2 * kRouterTokens;
+    if (tokens <= 0 || (tokens + tile - 1) / tile * experts > kRankedPrefixMax) return 0;
+    return tile;
+}
+
 int launch_router_fused(const uint16_t* x, const float* router_w, const float* bias,
                         int32_t* ids32, int64_t* ids64, float* weights, float* logits_out,
                         uint16_t* planes, int64_t tokens, int hidden, int experts, int topk,
-                        hipStream_t stream) {
+                        int32_t* ranks, int32_t* tile_counts, hipStream_t stream) {
     if (tokens == 0) return MOE_OK;
     if (router_w != nullptr) {  // else planes already holds the split
         const int rc = launch_router_split(router_w, planes, experts, hidden, stream);
@@ -747,18 +828,19 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
                                                    router_partials_offset(experts, hidden));
         hipLaunchKernelGGL((router_ring_kernel<1, 1, true>), dim3(static_cast<unsigned>(tiles * slices)),
                            dim3(256), 0, stream, x, planes, bias, ids32, ids64, weights, logits_out, tokens,
-                           hidden, experts, topk, partials, slices, per);
+                           hidden, experts, topk, partials, slices, per, nullptr, nullptr);
         const int rs = check_launch("router_ring_kernel");
         if (rs != MOE_OK) return rs;
         hipLaunchKernelGGL(router_reduce_kernel, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream,
-                           partials, bias, ids32, ids64, weights, logits_out, tokens, experts, topk, slices);
+                           partials, bias, ids32, ids64, weights, logits_out, tokens, experts, topk, slices,
+                           ranks, tile_counts);
         return check_launch("router_reduce_kernel");
     }
 #define MOE_ROUTER_CASE(NTV, MTV)                                                                      \
     hipLaunchKernelGGL((router_ring_kernel<NTV, MTV>),                                                 \
                        dim3(static_cast<unsigned>((tokens + kRouterTokens * MTV - 1) / (kRouterTokens * MTV))), \
                        dim3(256), 0, stream, x, planes, bias, ids32, ids64, weights, logits_out, tokens, \
-                       hidden, experts, topk, nullptr, 1, 0)
+                       hidden, experts, topk, nullptr, 1, 0, ranks, tile_counts)
     // E <= 16 and hidden <= 8192: the VGPR-load kernel, 16 tokens per block.
     // Otherwise the LDS ring: one token tile per block for E <= 16 (the four
     // waves split k), two above (the waves split the 16x16 output tiles).
@@ -770,7 +852,7 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
         const int f = router_fragments(experts);
 #define MOE_DIRECT_CASE(P, FV)                                                                              \
     hipLaunchKernelGGL((router_direct_kernel<P, FV>), grid, dim3(kDirectWaves * 64), 0, stream, x, frags, \
-                       bias, ids32, ids64, weights, logits_out, tokens, hidden, experts, topk)
+                       bias, ids32, ids64, weights, logits_out, tokens, hidden, experts, topk, ranks, tile_counts)
 #define MOE_DIRECT_PER(FV)                    \
     if (per <= 2) MOE_DIRECT_CASE(2, FV);       \
     else if (per <= 4) MOE_DIRECT_CASE(4, FV);  \

@@ -95,6 +95,9 @@ class HipExtension:
         buffer is allocated for this call. ``router_weight=None`` reuses the
         split ``scratch`` already holds from an earlier call with the same E, H.
         """
+        self._router_fused(x, router_weight, bias, ids32, ids64, weights, logits, scratch, None)
+
+    def _router_fused(self, x, router_weight, bias, ids32, ids64, weights, logits, scratch, ranked):
         _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,
                "expected BF16 GPU x[T,H]")
         tokens, hidden = x.shape
@@ -124,11 +127,34 @@ class HipExtension:
         if scratch is None:
             scratch = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
         _check_gpu_tensor(scratch, x, "scratch")
-        status = self.lib.moe_router_fused(
-            _ptr(x), _ptr(router_weight), _ptr(bias), _ptr(ids32), _ptr(ids64), _ptr(weights),
-            _ptr(logits), _ptr(scratch), scratch.numel() * scratch.element_size(), tokens, hidden,
-            experts, topk, _stream(x.device))
+        args = (_ptr(x), _ptr(router_weight), _ptr(bias), _ptr(ids32), _ptr(ids64), _ptr(weights),
+                _ptr(logits), _ptr(scratch), scratch.numel() * scratch.element_size(), tokens, hidden,
+                experts, topk)
+        if ranked is None:
+            status = self.lib.moe_router_fused(*args, _stream(x.device))
+        else:
+            ranks, tile_counts = ranked
+            status = self.lib.moe_router_fused_ranked(*args, _ptr(ranks), _ptr(tile_counts),
+                                                      tile_counts.numel() * 4, _stream(x.device))
         self.lib.check(status, "router_fused_out")
+
+    def router_rank_tile(self, tokens, experts):
+        """Tokens per tile of a ranked route for (T, E), or 0 when the shape has none."""
+        return int(self.lib.moe_router_rank_tile(tokens, experts))
+
+    def router_fused_ranked_out(self, x, router_weight, bias, ids32, ids64, weights, ranks, tile_counts,
+                                logits=None, scratch=None):
+        """``router_fused_out`` that also writes the dispatch's in-tile ranks into
+        ``ranks`` (int32 [T*K]) and per-tile expert counts into ``tile_counts``
+        (int32, at least ceil(T / router_rank_tile(T, E)) * E), for
+        ``CudaWorkspace.dispatch_ranked``."""
+        tokens = x.shape[0] if x.dim() == 2 else -1
+        topk = ids32.shape[1] if ids32.dim() == 2 else -1
+        for name, t, n in (("ranks", ranks, tokens * topk), ("tile_counts", tile_counts, None)):
+            _check_gpu_tensor(t, x, name)
+            _check(t.dtype == torch.int32 and t.is_contiguous() and (n is None or t.numel() == n),
+                   f"expected contiguous int32 {name}" + (f"[{n}]" if n is not None else ""))
+        self._router_fused(x, router_weight, bias, ids32, ids64, weights, logits, scratch, (ranks, tile_counts))
 
     def router_split_out(self, router_weight, scratch):
         """Write the bf16 split of ``router_weight`` [E,H] fp32 into ``scratch`` alone (no routing)."""

@@ -13,7 +13,7 @@ from functools import lru_cache
 from pathlib import Path
 
 LIBRARY_NAME = "libmoe_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -32,6 +32,8 @@ _SIGNATURES = {
     "moe_router_scratch_bytes": (_i64, [_i64, _i64]),
     "moe_router_fused": (_int, [_c_void_p] * 8 + [_i64] * 5 + [_c_void_p]),
     "moe_router_split": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p]),
+    "moe_router_rank_tile": (_i64, [_i64, _i64]),
+    "moe_router_fused_ranked": (_int, [_c_void_p] * 8 + [_i64] * 5 + [_c_void_p, _c_void_p, _i64, _c_void_p]),
     "moe_dispatch_scratch_bytes": (_i64, [_i64, _i64, _i64]),
     "moe_dispatch": (
         _int,
@@ -40,6 +42,10 @@ _SIGNATURES = {
     "moe_dispatch_noalloc": (
         _int,
         [_c_void_p, _int] + [_c_void_p] * 6 + [_i64] * 6 + [_int, _c_void_p],
+    ),
+    "moe_dispatch_ranked": (
+        _int,
+        [_c_void_p, _int] + [_c_void_p] * 8 + [_i64] * 8 + [_int, _c_void_p],
     ),
     "moe_combine": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 4 + [_c_void_p]),
     "moe_swiglu": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),

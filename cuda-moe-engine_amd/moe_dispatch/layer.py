@@ -152,6 +152,12 @@ class MoEBlock(torch.nn.Module):
         self.routing_bias.copy_(bias)
 
     def route(self, x):
+        return self._route(x)
+
+    def _route(self, x, ranked_into=None):
+        """route(); with a CudaWorkspace whose shape has a ranked route
+        (``rank_tile`` > 0), the fused router also writes that workspace's
+        in-tile ranks and tile counts for its ``dispatch_ranked``."""
         if self.implementation == "cuda_fused":
             key = (x.shape[0], x.device)
             if key not in self._route_buffers:
@@ -167,10 +173,14 @@ class MoEBlock(torch.nn.Module):
                 self._router_scratch = torch.empty(need, dtype=torch.uint8, device=x.device)
                 self._router_split_of = None
             router_weight, split_of = self._router_split_plan()
-            self._extension.router_fused_out(
-                x, None if router_weight is None else self.router_weight, self.routing_bias, ids32, ids64,
-                weights, scratch=self._router_scratch,
-            )
+            weight = None if router_weight is None else self.router_weight
+            if ranked_into is None:
+                self._extension.router_fused_out(x, weight, self.routing_bias, ids32, ids64, weights,
+                                                 scratch=self._router_scratch)
+            else:
+                self._extension.router_fused_ranked_out(x, weight, self.routing_bias, ids32, ids64, weights,
+                                                        ranked_into.tile_ranks, ranked_into.tile_counts,
+                                                        scratch=self._router_scratch)
             self._router_split_of = split_of
             return ids32, ids64, weights
         logits = torch.nn.functional.linear(x.float(), self.router_weight) + self.routing_bias
@@ -270,8 +280,13 @@ class MoEBlock(torch.nn.Module):
             if launches is not None and launches.still_valid(self):
                 return launches(self, x)
         state = self.workspace(x)
-        ids32, ids64, weights = self.route(x)
-        state.transport.dispatch(x, ids32, ids64)
+        # The fused router does the dispatch's counting pass when the shape allows.
+        ranked = self.implementation == "cuda_fused" and state.transport.rank_tile > 0
+        ids32, ids64, weights = self._route(x, state.transport if ranked else None)
+        if ranked:
+            state.transport.dispatch_ranked(x, ids32)
+        else:
+            state.transport.dispatch(x, ids32, ids64)
         output = self.experts_forward(state)
         state.transport.combine(output, weights)
         if self.implementation == "cuda_fused":
@@ -313,10 +328,19 @@ class _FusedLaunches:
         self.router = (block.routing_bias.data_ptr(), ids32.data_ptr(), ids64.data_ptr(), weights.data_ptr(),
                        None, scratch.data_ptr(), scratch.numel() * scratch.element_size(),
                        tokens, hidden, cfg.experts, cfg.topk)
-        self.dispatch = (_lib.DTYPE_BF16, ids32.data_ptr(), t.counts.data_ptr(), t.offsets.data_ptr(), t.slots.data_ptr(),
-                         t.packed.data_ptr(), t.inverse.data_ptr(), t.scratch.data_ptr(),
-                         t.scratch.numel() * t.scratch.element_size(), tokens, hidden, cfg.experts, cfg.topk,
-                         t.alignment, rows, int(bool(t.vectorized)))
+        # A ranked route (the router counts for the dispatch) whenever the shape has one, as in forward().
+        self.ranked = t.rank_tile > 0
+        if self.ranked:
+            self.router += (t.tile_ranks.data_ptr(), t.tile_counts.data_ptr(), t.tile_counts.numel() * 4)
+            self.dispatch = (_lib.DTYPE_BF16, ids32.data_ptr(), t.counts.data_ptr(), t.offsets.data_ptr(),
+                             t.slots.data_ptr(), t.packed.data_ptr(), t.inverse.data_ptr(), t.tile_ranks.data_ptr(),
+                             t.tile_counts.data_ptr(), t.tile_counts.numel() * 4, t.rank_tile, tokens, hidden,
+                             cfg.experts, cfg.topk, t.alignment, rows, int(bool(t.vectorized)))
+        else:
+            self.dispatch = (_lib.DTYPE_BF16, ids32.data_ptr(), t.counts.data_ptr(), t.offsets.data_ptr(),
+                             t.slots.data_ptr(), t.packed.data_ptr(), t.inverse.data_ptr(), t.scratch.data_ptr(),
+                             t.scratch.numel() * t.scratch.element_size(), tokens, hidden, cfg.experts, cfg.topk,
+                             t.alignment, rows, int(bool(t.vectorized)))
         self.gateup = (t.packed.data_ptr(), block.gate_up_weight.data_ptr(), state.activated.data_ptr(),
                        t.offsets.data_ptr(), rows, hidden, cfg.intermediate, cfg.experts)
         self.down = (state.activated.data_ptr(), block.down_weight.data_ptr(), state.expert_output.data_ptr(),
@@ -344,9 +368,14 @@ class _FusedLaunches:
         stream = current_stream_handle(self.device_index)
         x_ptr = x.data_ptr()
         router_weight, split_of = block._router_split_plan()
-        lib.check(lib.moe_router_fused(x_ptr, router_weight, *self.router, stream), "router_fused_out")
-        block._router_split_of = split_of
-        lib.check(lib.moe_dispatch(x_ptr, *self.dispatch, stream), "dispatch")
+        if self.ranked:
+            lib.check(lib.moe_router_fused_ranked(x_ptr, router_weight, *self.router, stream), "router_fused_out")
+            block._router_split_of = split_of
+            lib.check(lib.moe_dispatch_ranked(x_ptr, *self.dispatch, stream), "dispatch")
+        else:
+            lib.check(lib.moe_router_fused(x_ptr, router_weight, *self.router, stream), "router_fused_out")
+            block._router_split_of = split_of
+            lib.check(lib.moe_dispatch(x_ptr, *self.dispatch, stream), "dispatch")
         lib.check(lib.moe_grouped_gateup_swiglu(*self.gateup, stream), "gateup_swiglu_out")
         lib.check(lib.moe_grouped_gemm(*self.down, stream), "grouped_gemm_out")
         lib.check(lib.moe_combine(*self.combine, stream), "combine_out")

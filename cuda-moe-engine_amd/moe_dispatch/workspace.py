@@ -15,6 +15,11 @@ raising ``RuntimeError``) and makes one ctypes call on the current stream.
 Expert ids are not range-checked here (the kernels skip out-of-range ids, as
 the reference's do); ``ops.dispatch`` checks them.
 
+A workspace also holds the buffers of a ranked route (``tile_ranks``,
+``tile_counts``; ``rank_tile`` tokens per tile, 0 when the shape has none):
+the fused router can write the in-tile ranks and per-tile counts itself,
+after which ``dispatch_ranked`` runs only the pack pass.
+
 One workspace serves one invocation at a time: its outputs are views that the
 next call overwrites.
 """
@@ -71,6 +76,10 @@ class _Bound:
                           ws.packed.data_ptr(), ws.inverse.data_ptr(), ws.scratch.data_ptr(), nbytes,
                           tokens, hidden, experts, topk, ws.alignment, ws.capacity_rows,
                           int(bool(ws.vectorized)))
+        self.ranked_after_ids = (ws.counts.data_ptr(), ws.offsets.data_ptr(), ws.slots.data_ptr(),
+                                 ws.packed.data_ptr(), ws.inverse.data_ptr(), ws.tile_ranks.data_ptr(),
+                                 ws.tile_counts.data_ptr(), ws.tile_counts.numel() * 4, ws.rank_tile, tokens,
+                                 hidden, experts, topk, ws.alignment, ws.capacity_rows, int(bool(ws.vectorized)))
         self.output = ws.output.data_ptr()
         self.inverse = ws.inverse.data_ptr()
         self.x_shape = (tokens, hidden)
@@ -95,6 +104,13 @@ class _Bound:
         self._require(ids32, self.ids_shape, torch.int32, "ids")
         status = self.lib.moe_dispatch(x.data_ptr(), self.code, ids32.data_ptr(), *self.after_ids,
                                        current_stream_handle(self.device_index))
+        self.lib.check(status, self.name)
+
+    def dispatch_ranked(self, x, ids32):
+        self._require(x, self.x_shape, self.dtype, "x")
+        self._require(ids32, self.ids_shape, torch.int32, "ids")
+        status = self.lib.moe_dispatch_ranked(x.data_ptr(), self.code, ids32.data_ptr(), *self.ranked_after_ids,
+                                              current_stream_handle(self.device_index))
         self.lib.check(status, self.name)
 
     def combine(self, expert_output, weights):
@@ -132,6 +148,9 @@ class CudaWorkspace:
         self.extension = extension if extension is not None else get_extension()
         rows = self.capacity_rows
         assignments = tokens * topk
+        # Tokens per tile of a ranked route for this shape (0: none) and its count table.
+        self.rank_tile = self.extension.router_rank_tile(tokens, experts)
+        tiles = -(-tokens // self.rank_tile) if self.rank_tile > 0 else 0
         # name -> (shape, dtype); `scratch` holds the dispatch kernels' per-chunk count table.
         layout = {
             "counts": ((experts,), torch.int32),
@@ -141,6 +160,8 @@ class CudaWorkspace:
             "inverse": ((tokens, topk), torch.int32),
             "output": ((tokens, hidden), dtype),
             "scratch": ((max(self.extension.scratch_bytes(tokens, experts, topk), 4),), torch.uint8),
+            "tile_ranks": ((assignments if tiles else 1,), torch.int32),
+            "tile_counts": ((max(tiles * experts, 1),), torch.int32),
         }
         self._names = tuple(layout)
         for name, (shape, kind) in layout.items():
@@ -150,6 +171,13 @@ class CudaWorkspace:
     def dispatch(self, x, ids32, ids64=None):
         """Hot path: contiguous x[T,H] and int32 ids[T,K] with in-range ids (ids64 is unused)."""
         self._bound.dispatch(x, ids32)
+
+    def dispatch_ranked(self, x, ids32):
+        """dispatch() after a ranked route that wrote this workspace's ``tile_ranks``
+        and ``tile_counts`` for these ids (``rank_tile`` > 0): the pack pass only."""
+        if self.rank_tile <= 0:
+            raise RuntimeError("this workspace's shape has no ranked route (rank_tile == 0)")
+        self._bound.dispatch_ranked(x, ids32)
 
     def combine(self, expert_output, weights):
         """Hot path: expert_output[R, H] (R >= T*K) of the workspace dtype, fp32 weights[T,K]."""

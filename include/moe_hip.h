@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 5
+#define MOE_ABI_VERSION 6
 
 typedef enum {
     MOE_DTYPE_F32 = 0,
@@ -75,7 +75,8 @@ int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64
 
 /* Bytes of scratch moe_router_fused needs for (E, H): the bf16 split of
  * router_w, then 64 KiB of partial logits for the small-batch (T <= 64,
- * E <= 16) split-k path. */
+ * E <= 16) split-k path, then for E <= 16 a copy of the split in the MFMA
+ * operand order the E <= 16 kernel reads (ceil(H/64) * ceil(6E/16) KiB). */
 int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden);
 
 /*
@@ -105,6 +106,31 @@ int moe_router_fused(const void* x, const float* router_w, const float* bias, in
  */
 int moe_router_split(const float* router_w, void* scratch, int64_t scratch_bytes, int64_t experts,
                      int64_t hidden, void* stream);
+
+/*
+ * Tokens per tile of moe_router_fused_ranked for (T, E): 16 for E <= 16, 32
+ * above, or 0 when ceil(T / tile) * E > 4096 or T == 0 (then route with
+ * moe_router_fused and dispatch with moe_dispatch); -1 for invalid E or T.
+ * No counterpart in the reference.
+ */
+int64_t moe_router_rank_tile(int64_t tokens, int64_t experts);
+
+/*
+ * moe_router_fused that also does the counting pass of the dispatch for the
+ * routes it selects: for each tile of `tile` = moe_router_rank_tile(T, E)
+ * consecutive tokens, tile_counts[tile_index * E + e] = the tile's
+ * assignments to expert e, and ranks[p] = #{p' < p in p's tile : ids[p'] ==
+ * ids[p]} (flat order p = t*K + k; ranks holds T*K int32). moe_dispatch_ranked
+ * then skips its own counting pass (one launch less per forward).
+ * tile_counts_bytes >= ceil(T / tile) * E * 4; MOE_ERR_UNSUPPORTED when
+ * moe_router_rank_tile returns 0. No counterpart in the reference (its router
+ * and dispatch are separate passes).
+ */
+int moe_router_fused_ranked(const void* x, const float* router_w, const float* bias, int32_t* ids32,
+                            int64_t* ids64, float* weights, float* logits_out, void* scratch,
+                            int64_t scratch_bytes, int64_t tokens, int64_t hidden, int64_t experts,
+                            int64_t topk, int32_t* ranks, int32_t* tile_counts, int64_t tile_counts_bytes,
+                            void* stream);
 
 /* Bytes of scratch moe_dispatch needs for (T, E, K). */
 int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk);
@@ -148,6 +174,23 @@ int moe_dispatch_noalloc(const void* x, int dtype, const int32_t* ids, int32_t* 
                          int32_t* offsets, int32_t* slots, void* packed, int32_t* inverse,
                          int64_t tokens, int64_t hidden, int64_t experts, int64_t topk,
                          int64_t alignment, int64_t packed_rows, int vectorized, void* stream);
+
+/*
+ * moe_dispatch after moe_router_fused_ranked: ids, ranks and tile_counts are
+ * that call's outputs and tile_tokens its tile (moe_router_rank_tile(T, E);
+ * other values return MOE_ERR_INVALID_ARGUMENT). Runs only the pack pass
+ * (reference csrc/dispatch.cu:218-275, with the count and scan of :13-53
+ * folded into the router); counts, offsets, slots, inverse and packed are
+ * moe_dispatch's, bit for bit. ranks is only read, so the call can be
+ * repeated. No scratch argument: the tile table is the count table.
+ * Destination and padding rows stay below packed_rows whatever ranks and
+ * tile_counts hold. No counterpart in the reference.
+ */
+int moe_dispatch_ranked(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
+                        int32_t* slots, void* packed, int32_t* inverse, const int32_t* ranks,
+                        const int32_t* tile_counts, int64_t tile_counts_bytes, int64_t tile_tokens, int64_t tokens,
+                        int64_t hidden, int64_t experts, int64_t topk, int64_t alignment, int64_t packed_rows,
+                        int vectorized, void* stream);
 
 /*
  * Weighted combine: out[t] = round(sum_k w[t,k] * float(y[inverse[t,k]])),

@@ -82,6 +82,33 @@ def test_validation_errors_without_launching():
     assert lib.moe_set_gemm_workgroups(16) == 0 and lib.moe_set_gemm_workgroups(0) == 0
 
 
+def test_ranked_route_arguments_are_checked_without_launching():
+    lib = _lib.load_library()
+    # Tile size: 16 tokens for E <= 16, 32 above; none past 4096 table entries or for no tokens.
+    assert lib.moe_router_rank_tile(4096, 8) == 16 and lib.moe_router_rank_tile(4096, 16) == 16
+    assert lib.moe_router_rank_tile(100, 64) == 32 and lib.moe_router_rank_tile(2048, 64) == 32
+    assert lib.moe_router_rank_tile(2049, 64) == 0 and lib.moe_router_rank_tile(8192, 64) == 0
+    assert lib.moe_router_rank_tile(0, 8) == 0
+    assert lib.moe_router_rank_tile(10, 65) == -1 and lib.moe_router_rank_tile(-1, 8) == -1
+    need = lib.moe_router_scratch_bytes(8, 64)
+    # Router: 100 tokens, E=8 -> 7 tiles x 8 counts x 4 bytes = 224 bytes.
+    args = (16, 16, 16, 16, 16, 16, None, 16, need, 100, 64, 8, 2)
+    assert lib.moe_router_fused_ranked(*args, 16, 16, 223, None) == 4
+    assert b"224" in lib.moe_last_error()
+    assert lib.moe_router_fused_ranked(*args, None, 16, 224, None) == 1
+    assert lib.moe_router_fused_ranked(*args, 18, 16, 224, None) == 1  # ranks not 4-byte aligned
+    big = (16, 16, 16, 16, 16, 16, None, 16, lib.moe_router_scratch_bytes(64, 64), 8192, 64, 64, 6)
+    assert lib.moe_router_fused_ranked(*big, 16, 16, 1 << 30, None) == 2  # no ranked route for this shape
+    # Dispatch: the tile must be the route's; then the table size.
+    d = (16, 2, 16, 16, 16, 16, 16, 16, 16, 16)
+    tail = (100, 64, 8, 2, 1, 200, 1, None)
+    assert lib.moe_dispatch_ranked(*d, 224, 32, *tail) == 1
+    assert b"not the ranked route's tile" in lib.moe_last_error()
+    assert lib.moe_dispatch_ranked(*d, 223, 16, *tail) == 4
+    assert lib.moe_dispatch_ranked(16, 2, 16, 16, 16, 16, 16, 16, None, 16, 224, 16, *tail) == 1
+    assert lib.moe_dispatch_ranked(*d, 224, 16, 100, 64, 8, 2, 1, 199, 1, None) == 4  # packed rows
+
+
 def test_misaligned_pointers_are_rejected_without_launching():
     """Addresses the kernels cannot access as they must are refused before any launch.
 
