@@ -139,7 +139,7 @@ int64_t moe_dispatch_scratch_bytes(int64_t tokens, int64_t experts, int64_t topk
  * Token dispatch: expert histogram, prefix scan and stable pack.
  * Replaces dispatch_out (alignment == 1; reference csrc/dispatch.cu:102-158)
  * and dispatch_aligned_out (alignment > 1; :218-275), binding
- * csrc/bindings.cpp:2-4,7-9.
+ * csrc/bindings.cpp:3-5,8-10.
  *   counts[e]  = #{p : ids[p] == e}
  *   offsets[0] = 0, offsets[e+1] = offsets[e] + ceil(counts[e]/a)*a
  *   slots[p]   = #{p' < p : ids[p'] == ids[p]}     (canonical order)
@@ -197,7 +197,7 @@ int moe_dispatch_ranked(const void* x, int dtype, const int32_t* ids, int32_t* c
  * fp32 products and running sum in k order (no fused multiply-add), rows
  * outside [0, packed_rows) skipped, no atomics.
  * Replaces combine_out (reference csrc/dispatch.cu:160-192, kernel :76-93;
- * binding csrc/bindings.cpp:5-6).
+ * binding csrc/bindings.cpp:6-7).
  */
 int moe_combine(const void* expert_output, int dtype, const int32_t* inverse,
                 const float* weights, void* output, int64_t tokens, int64_t hidden,
@@ -207,7 +207,7 @@ int moe_combine(const void* expert_output, int dtype, const int32_t* inverse,
  * SwiGLU: out[r, j] = round(silu(g) * u), g = proj[r, j], u = proj[r, I + j],
  * fp32 math, one cast; rows >= *valid_rows (device int32) are exactly zero.
  * Replaces swiglu_out (reference csrc/dispatch.cu:294-323, kernel :277-292;
- * binding csrc/bindings.cpp:10).
+ * binding csrc/bindings.cpp:11).
  */
 int moe_swiglu(const void* projection, int dtype, const int32_t* valid_rows, void* output,
                int64_t rows, int64_t width, void* stream);
