@@ -502,8 +502,8 @@ __global__ __launch_bounds__(256) void router_ring_kernel(
 // 16x16x32 product covers 8 tokens and a 64-k step: operand row 2t + h is
 // token t's k half h (k0 + 32h ..), so the eight lanes of a token read one
 // whole 128-byte line and a token load reads 8 full lines; a layout with one
-// token per row reads 64 bytes of 16 lines, and took 1.4x longer at H=4096,
-// 4096 tokens. The weight operand's column 2r + h holds plane row r (r = q*E
+// token per row reads 64 bytes of 16 lines (H=4096, 4096 tokens: 9.1 against
+// 7.7 us). The weight operand's column 2r + h holds plane row r (r = q*E
 // + e: plane q, expert e) at k half h, so output (2t + h, 2r + h) is token t's
 // k-half-h product with plane row r (the other outputs mix the halves and are
 // not used). The planes are read from a copy in this fragment order
