@@ -1,6 +1,6 @@
 """MoE block forward benchmark on one MI355X (implementation="cuda_fused").
 
-Workload (BASELINE metric configuration): H=4096, I=14336, E=8, top-2,
+Workload (the headline metric's configuration): H=4096, I=14336, E=8, top-2,
 T=4096 tokens, bf16 x ~ N(0,1), random-init weights of that architecture
 (router fp32 ~ N(0,1/H), gate_up/down bf16 ~ N(0,1/fan_in)), zero router bias.
 Inputs and weights are resident in HBM before timing starts.
@@ -9,8 +9,9 @@ Prints ONE JSON line: value = mean forward latency (us) over the timed steps,
 plus per-stage latencies, expert-GEMM TFLOP/s, dispatch/combine GB/s, the
 roofline of the dominant kernel (gate/up GEMM with the SwiGLU epilogue, timed
 with events on the stream it is launched on), the PyTorch variant on the same
-GPU, and a CPU baseline: the same PyTorch variant on the host CPU at BASELINE
-config 1 (all cores and one thread), plus a token sample of this workload.
+GPU, and a CPU baseline: the same PyTorch variant on the host CPU at the
+reference's CPU-runnable configuration (T=128, H=512, I=1024, E=8, top-2; all
+cores and one thread), plus a token sample of this workload.
 """
 
 from __future__ import annotations
@@ -199,7 +200,7 @@ def _time_cpu(fn, warmup, samples):
 def cpu_baseline(gpu_block=None, gpu_x=None, c4_sample_tokens=64):
     """The PyTorch variant (implementation="torch", F.grouped_mm) on the host CPU.
 
-    Main figure: BASELINE config 1 (T=128, H=512, I=1024, E=8, top-2, bf16, seed 0),
+    Main figure: the reference's CPU-runnable configuration (T=128, H=512, I=1024, E=8, top-2, bf16, seed 0),
     every token, 10 warm-ups + 40 perf_counter_ns samples, with all the CPUs this
     process may use and again with 1 thread. When the benchmark's own block is
     given, the same variant also runs on its first `c4_sample_tokens` tokens with
@@ -228,7 +229,7 @@ def cpu_baseline(gpu_block=None, gpu_x=None, c4_sample_tokens=64):
             "cores": threads,
             "kind": "port",
             "sample": "this repo's PyTorch variant of the reference block (implementation='torch': topk/softmax "
-                      "router, stable-sort transport, F.grouped_mm experts, fp32 combine) at BASELINE config 1 "
+                      "router, stable-sort transport, F.grouped_mm experts, fp32 combine) at benchmark config 1 "
                       "(T=128 H=512 I=1024 E=8 top-2 bf16, seed 0), all 128 tokens, no scaling; median of 40 "
                       "perf_counter_ns samples after 10 warm-ups",
             "config": {"tokens": 128, "hidden": 512, "intermediate": 1024, "experts": 8, "topk": 2,

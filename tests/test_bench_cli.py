@@ -81,7 +81,7 @@ def test_byte_models_and_workload_bias_equal_the_oracle():
 
 
 def test_cpu_baseline_times_the_torch_variant_at_config_1(monkeypatch):
-    """The CPU baseline leg runs the PyTorch variant at BASELINE config 1 (shortened here)."""
+    """The CPU baseline leg runs the PyTorch variant at benchmark config 1 (T=128, H=512; shortened here)."""
     import torch
 
     calls = []

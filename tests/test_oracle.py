@@ -3,7 +3,7 @@
 Each oracle function is checked against something independent of its own
 formula: torch library routines (bf16 cast, topk, softmax, stable sort,
 bincount, matmul), pure-Python brute force on tiny inputs, the reference's
-known answers (zero-logit tie KAT, capacity rows of the BASELINE shapes), and
+known answers (zero-logit tie KAT, capacity rows of the benchmark shapes), and
 invariants of the reference's validate_case. Two mutation tests plant a
 plausible mistake in a copy of an oracle function and show the checks catch it.
 """
@@ -163,7 +163,7 @@ def test_dispatch_masks_out_of_range_ids():
 
 
 def test_capacity_rows_of_the_baseline_shapes():
-    """Capacity R of the BASELINE configurations (alignment 8; compact transport R = N)."""
+    """Capacity R of the benchmark configurations (alignment 8; compact transport R = N)."""
     assert oracle.capacity_rows(128, 8, 2, 8) == 320
     assert oracle.capacity_rows(4096, 8, 2, 1) == 8192
     assert [oracle.capacity_rows(t, 16, 2, 8) for t in (256, 1024, 4096)] == [632, 2168, 8312]
