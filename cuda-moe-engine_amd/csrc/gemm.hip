@@ -331,13 +331,13 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 }
 
 // The ring's shape and direct-to-LDS loads for one tile: rows [row0,
-// row0 + SMT*64) of one expert (clamped to row_end) by BNT weight rows from
+// row0 + TMR) of one expert (clamped to row_end) by BNT weight rows from
 // output column col0, in the first LDS_BYTES of `lds`, at most MAXS stages
 // deep. The four waves split the tile as (4/WC) row blocks x WC column blocks.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2, int MAXS = 4>
+template <int TMR, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2, int MAXS = 4>
 struct RingOps {
     static constexpr int WAVES = kRingThreads / kWave;
-    static constexpr int TM = SMT * 64;
+    static constexpr int TM = TMR;
     static constexpr int WTM = TM / (WAVES / WC);  // the four waves as (4/WC) x WC
     static constexpr int WTN = BNT / WC;
     static constexpr int FA = WTM / 16;       // 16-row A fragments per wave
@@ -476,13 +476,13 @@ struct NoHook {
 // tile of the same shape and k) into the slots that follow, so the next tile
 // starts at slots (sa0 + k_steps) % SA and (sb0 + k_steps) % SB and its hook
 // only issues the prologue's last window. Requires k_steps >= SB.
-template <int SMT, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4>
+template <int TMR, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end, bool own_prologue = true,
                                           bool wait_all = false, const Hook& hook = Hook{}, int sa0 = 0, int sb0 = 0,
                                           bool chain = false,
-                                          typename RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC, MAXS>::Rsrc next = {}) {
-    using R = RingOps<SMT, BNT, SWIGLU, LDS_BYTES, WC, MAXS>;
+                                          typename RingOps<TMR, BNT, SWIGLU, LDS_BYTES, WC, MAXS>::Rsrc next = {}) {
+    using R = RingOps<TMR, BNT, SWIGLU, LDS_BYTES, WC, MAXS>;
     constexpr int WTM = R::WTM, WTN = R::WTN, FA = R::FA, FB = R::FB;
     constexpr int A_LOADS = R::A_LOADS, B_LOADS = R::B_LOADS;
     constexpr int SA = R::SA, SB = R::SB;
@@ -971,17 +971,17 @@ __device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, co
     const int k_steps = static_cast<int>(p.k / kStageK);
     auto go = [&](auto ops) { ops.prologue(k_steps); };
     switch (w.variant) {
-        case 0: go(RingOps<4, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 1: go(RingOps<2, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 2: go(RingOps<1, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 0: go(RingOps<256, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 1: go(RingOps<128, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 2: go(RingOps<64, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         default:
             if constexpr (!SWIGLU) {
-                if (w.variant == 3) go(RingOps<4, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
-                else if (w.variant == 4) go(RingOps<2, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
-                else if (w.variant == 5) go(RingOps<1, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
-                else if (w.variant == 6) go(RingOps<4, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
-                else if (w.variant == 7) go(RingOps<2, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
-                else go(RingOps<1, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                if (w.variant == 3) go(RingOps<256, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else if (w.variant == 4) go(RingOps<128, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else if (w.variant == 5) go(RingOps<64, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else if (w.variant == 6) go(RingOps<256, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else if (w.variant == 7) go(RingOps<128, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
+                else go(RingOps<64, 64, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
             }
     }
 }
@@ -991,10 +991,10 @@ __device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, co
 // enough, the two are chained (see ring_tile): `w`'s last windows load `nxt`'s
 // first stages and its hook issues only the prologue's last window. Otherwise
 // the hook issues `nxt`'s whole prologue at slots 0.
-template <int SMT, int BNT, bool SWIGLU>
+template <int TMR, int BNT, bool SWIGLU>
 __device__ __forceinline__ void ring_run_shape(const GemmParams& p, char* lds, const RingWork& w,
                                                const RingWork& nxt, bool wait_all, int& sa, int& sb) {
-    using R = RingOps<SMT, BNT, SWIGLU, kRingBytes>;
+    using R = RingOps<TMR, BNT, SWIGLU, kRingBytes>;
     const int k_steps = static_cast<int>(p.k / kStageK);
     // Wave-uniform (it selects buffer resources, which live in SGPRs).
     const bool chain = __builtin_amdgcn_readfirstlane(nxt.valid && nxt.variant == w.variant && k_steps >= R::SB) != 0;
@@ -1008,7 +1008,7 @@ __device__ __forceinline__ void ring_run_shape(const GemmParams& p, char* lds, c
         else
             ring_prologue<SWIGLU>(p, lds, nxt);
     };
-    ring_tile<SMT, BNT, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook,
+    ring_tile<TMR, BNT, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook,
                                              sa, sb, chain, next);
     sa = chain ? na : 0;
     sb = chain ? nb : 0;
@@ -1018,17 +1018,17 @@ template <bool SWIGLU>
 __device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const RingWork& w, const RingWork& nxt,
                                          bool wait_all, int& sa, int& sb) {
     switch (w.variant) {
-        case 0: ring_run_shape<4, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 1: ring_run_shape<2, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 2: ring_run_shape<1, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 0: ring_run_shape<256, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 1: ring_run_shape<128, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 2: ring_run_shape<64, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         default:
             if constexpr (!SWIGLU) {
-                if (w.variant == 3) ring_run_shape<4, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 4) ring_run_shape<2, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 5) ring_run_shape<1, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 6) ring_run_shape<4, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 7) ring_run_shape<2, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else ring_run_shape<1, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
+                if (w.variant == 3) ring_run_shape<256, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 4) ring_run_shape<128, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 5) ring_run_shape<64, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 6) ring_run_shape<256, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else if (w.variant == 7) ring_run_shape<128, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
+                else ring_run_shape<64, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
             }
     }
 }
@@ -1164,24 +1164,24 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmP
     auto prologue = [&](const Work& w) {
         if constexpr (MAX_ROWS == 128) {
             if (w.tall) {
-                RingOps<2, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
+                RingOps<128, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
                     .prologue(k_steps);
                 return;
             }
         }
-        RingOps<1, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
+        RingOps<64, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
             .prologue(k_steps);
     };
     auto run = [&](const Work& w, bool wait_all, const auto& hook) {
         using Hook = std::decay_t<decltype(hook)>;
         if constexpr (MAX_ROWS == 128) {
             if (w.tall) {
-                ring_tile<2, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0,
+                ring_tile<128, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0,
                                                                                 w.row_end, false, wait_all, hook);
                 return;
             }
         }
-        ring_tile<1, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end,
+        ring_tile<64, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end,
                                                                         false, wait_all, hook);
     };
     int t = blockIdx.x;
