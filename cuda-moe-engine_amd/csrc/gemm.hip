@@ -881,7 +881,8 @@ __device__ __forceinline__ RingSlot ring_slot(const RingPlan& pl, int grid, int 
 struct RingWork {
     bool valid;
     int expert;
-    int variant;  // row tile 256 / 128 / 64 = 0 / 1 / 2; +3 for a 128-column piece, +6 for a 64-column one
+    int variant;  // row tile 256 / 128 / 64 = 0 / 1 / 2; +3 for a 128-column piece, +6 for a 64-column one;
+                  // 9: a whole 256-column tile of at most 32 rows
     int64_t row0, row_end, col0;
 };
 
@@ -949,7 +950,10 @@ __device__ __forceinline__ RingWork ring_locate(const GemmParams& p, const RingT
     w.row_end = min(static_cast<int64_t>(off) + span, p.rows);
     if (w.row0 < 0 || w.row0 >= w.row_end) return w;
     const int rem_rows = span - m_tile * 256;
-    w.variant = rem_rows > 128 ? 0 : (rem_rows > 64 ? 1 : 2);
+    // Short last tiles of at most 32 rows (at H=4096, 4096 tokens: 336 of the
+    // 448 gate/up short tiles) run a 32-row tile: half the MFMA work of the
+    // 64-row one. Column pieces keep the 64-row tile.
+    w.variant = rem_rows > 128 ? 0 : (rem_rows > 64 ? 1 : (rem_rows > 32 || s.piece >= 0 ? 2 : 9));
     if constexpr (SWIGLU) {
         w.col0 = static_cast<int64_t>(n_tile) * 128;
     } else if (s.piece < 0) {
@@ -974,6 +978,7 @@ __device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, co
         case 0: go(RingOps<256, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         case 1: go(RingOps<128, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         case 2: go(RingOps<64, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 9: go(RingOps<32, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         default:
             if constexpr (!SWIGLU) {
                 if (w.variant == 3) go(RingOps<256, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
@@ -1021,6 +1026,7 @@ __device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const R
         case 0: ring_run_shape<256, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         case 1: ring_run_shape<128, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         case 2: ring_run_shape<64, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 9: ring_run_shape<32, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         default:
             if constexpr (!SWIGLU) {
                 if (w.variant == 3) ring_run_shape<256, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
