@@ -676,6 +676,133 @@ __global__ __launch_bounds__(kDirectWaves * 64) void router_direct_kernel(
     }
 }
 
+// Fused router for 16 < E <= 64 on the same VGPR loads and fragment-order
+// planes as router_direct_kernel, organised for many experts: a block owns
+// 32 tokens (four groups of 8, two tokens per operand row as above) and its
+// four waves split the weight fragments (wave w: fragments w*FW .. w*FW+FW-1
+// of F = ceil(6E/16)), each over the whole k range, so no wave partials need
+// adding; every wave loads the four token fragments itself (they come from
+// L1/L2 after the first). Loads run up to about 40 ahead of the multiplies:
+// the LDS ring kernel this replaces (E = 64, H = 2048) held three 28 KiB
+// stages in flight per CU, and at about 2.5 us of load latency that bounded it
+// near 34 GB/s per CU (25-37 us at 8192 tokens).
+constexpr int kWideTokens = 32;
+constexpr int kWideWaves = 4;
+constexpr int kWideMaxPer = 64;  // 64-k steps: hidden <= 4096
+
+template <int PER, int FW>
+constexpr int wide_depth() {
+    constexpr int d = 40 / (4 + FW);
+    return d < PER ? d : PER;
+}
+
+template <int PER, int FW>
+__global__ __launch_bounds__(kWideWaves * 64) void router_wide_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ frags, const float* __restrict__ bias,
+    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, float* __restrict__ weights,
+    float* __restrict__ logits_out, int64_t tokens, int hidden, int experts, int topk, int32_t* __restrict__ ranks,
+    int32_t* __restrict__ tile_counts) {
+    constexpr int TB = kWideTokens, G = TB / 8, PR = 8 * FW * kWideWaves, PRP = 2 * PR + 1;
+    constexpr int D = wide_depth<PER, FW>();
+    static_assert(kWideWaves * 8 == TB, "the selection takes eight lanes per token");
+    __shared__ float part[TB][PRP];  // [token][half * PR + plane row]
+    __shared__ float sbias[kMaxExperts];
+    __shared__ int tile_ids[TB * kMaxTopk];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TB;
+    const int64_t rows = min(static_cast<int64_t>(TB), tokens - t0);
+    const uint32_t row_bytes = static_cast<uint32_t>(hidden) * 2;
+    const int steps = (hidden + 63) / 64;  // <= PER (the launcher's choice)
+    const int F = router_fragments(experts);
+    const __amdgpu_buffer_rsrc_t rsrc_x = make_rsrc(x + t0 * hidden, static_cast<uint32_t>(rows) * row_bytes);
+    const __amdgpu_buffer_rsrc_t rsrc_f = make_rsrc(frags, static_cast<uint32_t>(steps) * F * 1024u);
+    const int m = lane & 15, kq = lane >> 4, h = m & 1;
+    const int k_lane = h * 32 + kq * 8;
+    const uint32_t x_off = static_cast<uint32_t>(m >> 1) * row_bytes + k_lane * 2;
+    const int f0 = wave * FW;  // this wave's first fragment
+
+    struct Frag {
+        ru32x4_t a[G], b[FW];
+    };
+    auto load = [&](int s, Frag& fr) {
+        const bool in = s < steps;
+        const bool k_in = in && s * 64 + k_lane < hidden;
+        const uint32_t k_bytes = static_cast<uint32_t>(s) * 128;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            fr.a[g] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsrc_x, k_in ? x_off + g * 8 * row_bytes + k_bytes : kRouterOob, 0, 0);
+#pragma unroll
+        for (int f = 0; f < FW; ++f)
+            fr.b[f] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsrc_f, in && f0 + f < F ? static_cast<uint32_t>((s * F + f0 + f) * 64 + lane) * 16 : kRouterOob,
+                0, 0);
+    };
+    rfloatx4_t acc[G][FW];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int f = 0; f < FW; ++f) acc[g][f] = rfloatx4_t{0.f, 0.f, 0.f, 0.f};
+    Frag fr[D];
+    static_for<D>([&](auto u_c) { load(decltype(u_c)::value, fr[decltype(u_c)::value]); });
+    static_for<PER>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int f = 0; f < FW; ++f)
+                acc[g][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rbf16x8_t, fr[i % D].a[g]),
+                                                                    __builtin_bit_cast(rbf16x8_t, fr[i % D].b[f]),
+                                                                    acc[g][f], 0, 0, 0);
+        if constexpr (i + D < PER) load(i + D, fr[i % D]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    // As in router_direct_kernel: lane l holds rows 4*(l/16) + j and column
+    // 16f + l%16 of fragment f; the useful outputs have equal halves.
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int f = 0; f < FW; ++f)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int j = 2 * jj + h;
+                part[8 * g + 2 * kq + jj][h * PR + 8 * (f0 + f) + (m >> 1)] = acc[g][f][j];
+            }
+    if (threadIdx.x < experts) sbias[threadIdx.x] = bias[threadIdx.x];
+    __syncthreads();
+    constexpr int EPL = kMaxExperts / 8;
+    const int tl = wave * 8 + (lane >> 3);
+    const int sub = lane & 7;
+    const int64_t token = t0 + tl;
+    if (token < tokens) {  // uniform across each group of eight lanes
+        float v[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = sub * EPL + j;
+            v[j] = -INFINITY;
+            if (e < experts) {
+                float q[3];
+#pragma unroll
+                for (int p = 0; p < 3; ++p) {
+                    const int pr = p * experts + e;
+                    q[p] = part[tl][pr] + part[tl][PR + pr];
+                }
+                const float logit = (q[2] + q[1]) + q[0];
+                if (logits_out) logits_out[token * experts + e] = logit;
+                v[j] = logit + sbias[e];
+            }
+        }
+        select_eight_lanes<EPL>(v, sub, topk, token, ids32, ids64, weights, ranks ? tile_ids + tl * topk : nullptr);
+    }
+    if (ranks) {
+        __syncthreads();
+        if (threadIdx.x < kWave)
+            rank_tile(tile_ids, static_cast<int>(rows) * topk, t0 * topk, experts, ranks,
+                      tile_counts + static_cast<int64_t>(blockIdx.x) * experts);
+    }
+}
+
 // Sum of a token tile's k-slices in slice order, the bias, and the same
 // selection as router_ring_kernel (16 tokens x 16 expert slots, E <= 16).
 __global__ __launch_bounds__(256) void router_reduce_kernel(
@@ -760,8 +887,8 @@ int launch_topk_route(const float* logits, const float* bias, int32_t* ids32, in
 }
 
 // The three bf16 planes, then (256-byte aligned) the split path's partial
-// logits [tiles][slices][16 tokens][16 experts] fp32, then for E <= 16 the
-// planes in fragment order ([ceil(H/32)][F][64 lanes][16 bytes]).
+// logits [tiles][slices][16 tokens][16 experts] fp32, then the planes in
+// fragment order ([ceil(H/64)][F][64 lanes][16 bytes]).
 static int64_t router_partials_offset(int64_t experts, int64_t hidden) {
     return (3 * experts * hidden * 2 + 255) & ~static_cast<int64_t>(255);
 }
@@ -771,7 +898,7 @@ static int64_t router_fragments_offset(int64_t experts, int64_t hidden) {
 }
 
 static int64_t router_fragment_chunks(int64_t experts, int64_t hidden) {
-    return experts <= kDirectMaxExperts ? (hidden + 63) / 64 * router_fragments(static_cast<int>(experts)) * 64 : 0;
+    return (hidden + 63) / 64 * router_fragments(static_cast<int>(experts)) * 64;
 }
 
 int64_t router_scratch_bytes(int64_t experts, int64_t hidden) {
@@ -871,6 +998,31 @@ int launch_router_fused(const uint16_t* x, const float* router_w, const float* b
 #undef MOE_DIRECT_PER
 #undef MOE_DIRECT_CASE
         return check_launch("router_direct_kernel");
+    }
+    const int steps = (hidden + 63) / 64;
+    if (experts > kDirectMaxExperts && steps <= kWideMaxPer) {
+        const uint16_t* frags = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(planes) +
+                                                                  router_fragments_offset(experts, hidden));
+        const dim3 grid(static_cast<unsigned>((tokens + kWideTokens - 1) / kWideTokens));
+        const int fw = (router_fragments(experts) + kWideWaves - 1) / kWideWaves;
+#define MOE_WIDE_CASE(P, FV)                                                                              \
+    hipLaunchKernelGGL((router_wide_kernel<P, FV>), grid, dim3(kWideWaves * 64), 0, stream, x, frags, bias, \
+                       ids32, ids64, weights, logits_out, tokens, hidden, experts, topk, ranks, tile_counts)
+#define MOE_WIDE_PER(FV)                     \
+    if (steps <= 8) MOE_WIDE_CASE(8, FV);      \
+    else if (steps <= 16) MOE_WIDE_CASE(16, FV); \
+    else if (steps <= 32) MOE_WIDE_CASE(32, FV); \
+    else MOE_WIDE_CASE(64, FV);
+        switch (fw) {
+            case 2: MOE_WIDE_PER(2) break;
+            case 3: MOE_WIDE_PER(3) break;
+            case 4: MOE_WIDE_PER(4) break;
+            case 5: MOE_WIDE_PER(5) break;
+            default: MOE_WIDE_PER(6) break;
+        }
+#undef MOE_WIDE_PER
+#undef MOE_WIDE_CASE
+        return check_launch("router_wide_kernel");
     }
     if (experts <= 16) {
         MOE_ROUTER_CASE(1, 1);

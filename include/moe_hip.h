@@ -75,8 +75,8 @@ int moe_topk_route(const float* logits, const float* bias, int32_t* ids32, int64
 
 /* Bytes of scratch moe_router_fused needs for (E, H): the bf16 split of
  * router_w, then 64 KiB of partial logits for the small-batch (T <= 64,
- * E <= 16) split-k path, then for E <= 16 a copy of the split in the MFMA
- * operand order the E <= 16 kernel reads (ceil(H/64) * ceil(6E/16) KiB). */
+ * E <= 16) split-k path, then a copy of the split in the MFMA operand order
+ * the VGPR-load kernels read (ceil(H/64) * ceil(6E/16) KiB). */
 int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden);
 
 /*

@@ -66,12 +66,13 @@ def test_validation_errors_without_launching():
     assert lib.moe_router_fused(1, 1, 1, 1, 1, 1, None, 16, 1 << 20, 4, 12, 8, 2, None) == 2
     # Three bf16 planes (rounded up to 256 bytes), then the small-batch split's
     # fp32 partial logits: 4 token tiles x 16 slices x 16 tokens x 16 experts,
-    # then for E <= 16 the planes in fragment order: per 64 hidden, ceil(6E/16)
-    # fragments of 1 KiB.
+    # then the planes in fragment order: per 64 hidden, ceil(6E/16) fragments
+    # of 1 KiB.
     partials = 4 * 16 * 16 * 16 * 4
     assert lib.moe_router_scratch_bytes(8, 64) == 3 * 8 * 64 * 2 + partials + 1 * 3 * 1024
     assert lib.moe_router_scratch_bytes(5, 72) == 2304 + partials + 2 * 2 * 1024  # 2160 rounded up
-    assert lib.moe_router_scratch_bytes(17, 64) == 6656 + partials  # 6528 rounded up; no fragments above 16
+    assert lib.moe_router_scratch_bytes(17, 64) == 6656 + partials + 7 * 1024  # 6528 rounded up
+    assert lib.moe_router_scratch_bytes(64, 4096) == 3 * 64 * 4096 * 2 + partials + 64 * 24 * 1024
     assert lib.moe_router_scratch_bytes(65, 64) == -1
     need = lib.moe_router_scratch_bytes(8, 64)
     assert lib.moe_router_fused(16, 16, 16, 16, 16, 16, None, 16, need - 1, 4, 64, 8, 2, None) == 4

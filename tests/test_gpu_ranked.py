@@ -4,9 +4,9 @@
 tokens, the tile's expert counts and every assignment's rank among the
 tile's earlier assignments to the same expert (flat order p = t*K + k);
 ``CudaWorkspace.dispatch_ranked`` then runs only the pack pass. Checked here
-on every router kernel (VGPR-load kernel for E <= 16, split-k small batches,
-the LDS ring for hidden > 8192 and for E > 16 with 32-token tiles, ragged last
-tiles, alignment 1 and 8):
+on every router kernel (the VGPR-load kernels: 16-token tiles for E <= 16,
+32-token tiles above; split-k small batches; the LDS ring for hidden > 8192 at
+E <= 16 and hidden > 4096 above; ragged last tiles, alignment 1 and 8):
 
 * ranks and tile counts equal a numpy restatement of their definition;
 * ids, weights and the whole dispatch layout (counts, offsets, slots,
@@ -31,8 +31,9 @@ CASES = [
     (1000, 1024, 16, 2, 1),   # VGPR-load router, E = 16
     (40, 2048, 8, 2, 8),      # split-k router (T <= 64) and its selection kernel
     (130, 8200, 8, 2, 1),     # LDS ring router, E <= 16
-    (200, 256, 32, 4, 8),     # LDS ring router, E = 32: 32-token tiles
-    (100, 128, 64, 6, 1),     # LDS ring router, E = 64
+    (200, 256, 32, 4, 8),     # many-expert VGPR-load router, E = 32: 32-token tiles
+    (100, 128, 64, 6, 1),     # many-expert VGPR-load router, E = 64
+    (70, 4160, 32, 4, 8),     # LDS ring router, E = 32
     (17, 64, 5, 3, 16),       # one partial tile
 ]
 

@@ -76,7 +76,12 @@ def test_zero_logits_known_answer_and_empty_batch(ext):
      # (E = 2, 3, 8, 10, 12, 16) and 2, 8 and 16 steps of 64 hidden per wave (ragged
      # last token tile, k tail inside a step); hidden 8200 takes the ring.
      (300, 4096, 8, 2), (1000, 8192, 16, 2), (77, 200, 3, 2), (130, 8200, 8, 2), (90, 256, 2, 1),
-     (65, 320, 10, 3), (70, 64, 12, 4)],
+     (65, 320, 10, 3), (70, 64, 12, 4),
+     # 16 < E <= 64 and hidden <= 4096: the many-expert VGPR-load kernel with 2 to
+     # 6 fragments per wave (E = 17, 24, 40, 48; the last wave's range partly past
+     # F), 8 to 64 steps of 64 hidden, k tails, ragged token tiles; hidden 4160
+     # takes the ring.
+     (97, 1000, 17, 3), (33, 520, 24, 2), (129, 3000, 40, 6), (45, 4096, 48, 8), (50, 4160, 32, 4)],
 )
 def test_fused_router_matches_oracle(ext, tokens, hidden, experts, topk):
     generator = torch.Generator(device="cuda").manual_seed(tokens + hidden)
