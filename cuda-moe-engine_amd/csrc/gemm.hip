@@ -729,12 +729,13 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
 }
 
 // Work list, built on the device from offsets (the same in every workgroup).
-// Row tiles of more than 128 rows form phase 1: they all cost the same and are
-// compute-bound. The short last row tile of an expert (at most 128 rows) forms
-// phase 2: it reads a whole 256-row weight slab for a quarter or half of the
-// arithmetic, so its cost is streaming that slab at one CU's request rate
+// Row tiles of more than 128 rows form phase 1: they cost about the same and
+// are compute-bound. The short last row tile of an expert (at most 128 rows)
+// forms phase 2: it reads a whole 256-row weight slab for a quarter or half of
+// the arithmetic, so its cost is streaming that slab at one CU's request rate
 // (about half of a phase-1 tile: 49 vs 101 us at H=4096, I=14336), and many of
-// them at once are HBM-bound.
+// them at once are HBM-bound. With balanced row tiles (ring_table) only experts
+// of at most 128 rows have a phase-2 tile.
 //
 // The grid (G workgroups, workgroup i on XCD i % 8) walks virtual workgroups
 // q = blockIdx.x, blockIdx.x + G, ..., i.e. in rounds of G. Phase 1 is cut
@@ -882,14 +883,15 @@ struct RingWork {
     bool valid;
     int expert;
     int variant;  // row tile 256 / 128 / 64 = 0 / 1 / 2; +3 for a 128-column piece, +6 for a 64-column one;
-                  // 9: a whole 256-column tile of at most 32 rows
+                  // whole 256-column tiles of 32 / 224 / 192 / 160 rows = 9 / 10 / 11 / 12
     int64_t row0, row_end, col0;
 };
 
 struct RingTable {
-    int off, span, mf, s1, s2, c1, c2;  // lane e: expert e's first row, rows, full row tiles,
+    int off, span, mf, s1, s2, c1, c2;  // lane e: expert e's first row, rows, phase-1 row tiles,
                                         // first tile and tile count in phase 1 and 2
     int n_full, n_part;                 // tiles per phase (uniform)
+    bool balanced;                      // phase-1 row tiles of equal height (uniform)
 };
 
 __device__ __forceinline__ int wave_inclusive_sum(int x) {
@@ -902,8 +904,13 @@ __device__ __forceinline__ int wave_inclusive_sum(int x) {
     return x;
 }
 
-__device__ __forceinline__ RingTable ring_table(const GemmParams& p) {
+// Row tiles: ceil(rows / 256) per expert. Plain: 256-row tiles, the last in
+// phase 1 when it has more than 128 rows, else in phase 2. Balanced: an
+// expert of more than 128 rows has all its tiles in phase 1, of equal height
+// (ring_locate); one of at most 128 rows is a phase-2 tile.
+__device__ __forceinline__ RingTable ring_table(const GemmParams& p, bool balanced) {
     RingTable t;
+    t.balanced = balanced;
     const int lane = threadIdx.x & 63;
     t.off = 0;
     t.span = 0;
@@ -911,9 +918,10 @@ __device__ __forceinline__ RingTable ring_table(const GemmParams& p) {
         t.off = p.offsets[lane];
         t.span = max(p.offsets[lane + 1] - t.off, 0);
     }
-    t.mf = t.span / 256 + ((t.span % 256) > 128 ? 1 : 0);
+    const int tiles = (t.span + 255) / 256;
+    t.mf = balanced ? (t.span > 128 ? tiles : 0) : t.span / 256 + ((t.span % 256) > 128 ? 1 : 0);
     t.c1 = t.mf * p.n_tiles;
-    t.c2 = ((t.span + 255) / 256 - t.mf) * p.n_tiles;
+    t.c2 = (tiles - t.mf) * p.n_tiles;
     const int i1 = wave_inclusive_sum(t.c1), i2 = wave_inclusive_sum(t.c2);
     t.s1 = i1 - t.c1;
     t.s2 = i2 - t.c2;
@@ -938,22 +946,38 @@ __device__ __forceinline__ RingWork ring_locate(const GemmParams& p, const RingT
     const int mf = __builtin_amdgcn_readlane(t.mf, e);
     const int span = __builtin_amdgcn_readlane(t.span, e);
     const int off = __builtin_amdgcn_readlane(t.off, e);
-    int n_tile, m_tile;
+    // Phase 1: the expert's mf row tiles of h rows each (256, or balanced: the
+    // multiple of 32 that spreads the rows evenly, 160-256 when mf >= 2); the
+    // last may hold fewer. Phase 2: the expert's last tile (at most 128 rows).
+    int n_tile, m_tile, h;
     if (s.phase == 0) {
         n_tile = rel / mf;
         m_tile = rel - n_tile * mf;
+        h = t.balanced ? ((span + mf - 1) / mf + 31) / 32 * 32 : 256;
     } else {
         n_tile = rel;
         m_tile = mf;
+        h = 256;
     }
-    w.row0 = off + static_cast<int64_t>(m_tile) * 256;
-    w.row_end = min(static_cast<int64_t>(off) + span, p.rows);
+    w.row0 = off + static_cast<int64_t>(m_tile) * h;
+    w.row_end = min(min(w.row0 + h, static_cast<int64_t>(off) + span), p.rows);
     if (w.row0 < 0 || w.row0 >= w.row_end) return w;
-    const int rem_rows = span - m_tile * 256;
-    // Short last tiles of at most 32 rows (at H=4096, 4096 tokens: 336 of the
-    // 448 gate/up short tiles) run a 32-row tile: half the MFMA work of the
-    // 64-row one. Column pieces keep the 64-row tile.
-    w.variant = rem_rows > 128 ? 0 : (rem_rows > 64 ? 1 : (rem_rows > 32 || s.piece >= 0 ? 2 : 9));
+    if (s.phase != 0) h = static_cast<int>(w.row_end - w.row0);
+    // The tile runs the smallest row variant that holds h rows, so all row
+    // tiles of one expert run the same variant (and keep pace with each other).
+    // Phase-2 tiles of at most 32 rows (at H=4096, 4096 tokens: 336 of the 448
+    // gate/up short tiles) run a 32-row tile: half the MFMA work of the 64-row
+    // one. Column pieces exist for 256-, 128- and 64-row tiles.
+    if (s.piece >= 0)
+        w.variant = h > 128 ? 0 : (h > 64 ? 1 : 2);
+    else
+        w.variant = h > 224   ? 0
+                    : h > 192 ? 10
+                    : h > 160 ? 11
+                    : h > 128 ? 12
+                    : h > 64  ? 1
+                    : h > 32  ? 2
+                              : 9;
     if constexpr (SWIGLU) {
         w.col0 = static_cast<int64_t>(n_tile) * 128;
     } else if (s.piece < 0) {
@@ -979,6 +1003,9 @@ __device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, co
         case 1: go(RingOps<128, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         case 2: go(RingOps<64, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         case 9: go(RingOps<32, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 10: go(RingOps<224, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 11: go(RingOps<192, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 12: go(RingOps<160, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         default:
             if constexpr (!SWIGLU) {
                 if (w.variant == 3) go(RingOps<256, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
@@ -1027,6 +1054,9 @@ __device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const R
         case 1: ring_run_shape<128, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         case 2: ring_run_shape<64, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         case 9: ring_run_shape<32, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 10: ring_run_shape<224, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 11: ring_run_shape<192, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 12: ring_run_shape<160, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
         default:
             if constexpr (!SWIGLU) {
                 if (w.variant == 3) ring_run_shape<256, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
@@ -1042,7 +1072,13 @@ __device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const R
 template <bool SWIGLU>
 __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) char lds[kRingBytes];
-    const RingTable table = ring_table(p);
+    // Balanced row tiles for the gate/up GEMM at K >= 2048. There a short last
+    // tile's cost is streaming its 256 x K weight slab once more, and the
+    // expert's equal-height tiles share that slab in L2 instead (H=4096, I=14336,
+    // 4096 tokens: 1625 -> 1587 us; H=2048, I=1408, E=64 Zipf: 661 -> 651 us).
+    // Not at H=1024 (77 -> 81 us), nor for the down GEMM, whose short tiles run
+    // as column pieces on every CU (781 -> 800 us at H=4096, I=14336).
+    const RingTable table = ring_table(p, SWIGLU && p.k >= 2048);
     const int grid = static_cast<int>(gridDim.x);
     const RingPlan plan = ring_plan(table.n_full, table.n_part, grid, !SWIGLU);
     // The next tile of this workgroup at or after tile `sub` of virtual workgroup q.

@@ -95,6 +95,10 @@ SCHEDULE_CASES = [
     ([1030, 1030, 2048], 8, 512, 128, False, (8, 16)),
     # 6 full tiles beside 4 short ones: halves in the rounds from 16 workgroups on
     ([300, 40, 512], 8, 512, 128, False, (8, 16, 40)),
+    # gate/up at K = 2048: balanced row tiles of 160, 224, 192 and 256 rows
+    # (experts of 304, 424, 520 and 704 rows), 1040 rows as five of 224, and a
+    # phase-2 tile of 104 rows
+    ([300, 420, 520, 700, 1034, 100], 8, 136, 2048, True, (8, 24, 64)),
 ]
 
 
@@ -144,6 +148,8 @@ GATEUP_CASES = [
     ([700, 3, 0, 260], 8, 32, 384),
     ([129, 255, 256, 257], 8, 512, 136),
     ([2000, 17], 8, 1024, 1408),
+    # K = 2048: balanced row tiles (160 to 256 rows; five of 224 rows for 1040)
+    ([300, 420, 100, 1034, 520, 700, 0], 8, 2048, 136),
     # at most 128 rows in all: the 64-column decode tiles
     ([70, 9], 8, 96, 200),
     ([2, 0, 0, 1], 1, 512, 64),

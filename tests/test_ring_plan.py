@@ -8,10 +8,12 @@ tiles (phase 2); phase-2 tiles the rounds do not take, or phase 1 when there is
 no phase 2, run after the rounds with an optional split of a short last round
 into 128-column pieces (plain GEMM only); a phase 1 that fills at most half of
 one round beside a phase 2 runs in the rounds as 128-column halves (plain GEMM
-only). This restates those formulas and
-checks that every tile (or both halves of a split tile) is assigned exactly
-once for random expert layouts and grid sizes, that the rounds keep each XCD's
-phase-1 tiles in order, and that the measured shapes get the intended plans.
+only). The gate/up GEMM at K >= 2048 cuts each expert of more than 128 rows
+into ceil(rows/256) balanced row tiles, all in phase 1. This restates those
+formulas and checks that every tile (or both halves of a split tile) is
+assigned exactly once for random expert layouts and grid sizes, that the
+rounds keep each XCD's phase-1 tiles in order, that balanced tiles cover each
+expert's rows once, and that the measured shapes get the intended plans.
 The GPU test tests/test_gpu_gemm.py::test_schedule_does_not_change_results runs
 the kernel itself at the grid sizes used here.
 """
@@ -23,12 +25,25 @@ import pytest
 XCD = 8
 
 
-def phase_counts(counts, alignment, n_tiles):
+def phase_tiles(span, balanced):
+    """(phase-1 row tiles, their height) of one expert (ring_table, ring_locate)."""
+    tiles = -(-span // 256)
+    if not balanced:
+        return span // 256 + (1 if span % 256 > 128 else 0), 256
+    mf = tiles if span > 128 else 0
+    return mf, (-(-span // mf) + 31) // 32 * 32 if mf else 256
+
+
+def phase_counts(counts, alignment, n_tiles, balanced=False):
     spans = [(c + alignment - 1) // alignment * alignment for c in counts]
-    mf = [s // 256 + (1 if s % 256 > 128 else 0) for s in spans]
+    mf = [phase_tiles(s, balanced)[0] for s in spans]
     n1 = sum(m * n_tiles for m in mf)
-    n2 = sum(((s + 255) // 256 - m) * n_tiles for s, m in zip(spans, mf))
+    n2 = sum((-(-s // 256) - m) * n_tiles for s, m in zip(spans, mf))
     return n1, n2
+
+
+def balanced_for(swiglu, k):
+    return swiglu and k >= 2048
 
 
 def ring_phase(count, grid, allow_split, short_tiles=False):
@@ -145,8 +160,26 @@ def test_every_tile_runs_once(seed):
         experts = rng.randint(1, 64)
         counts = [rng.choice([0, rng.randint(1, 40), rng.randint(0, 600), rng.randint(0, 3000)])
                   for _ in range(experts)]
-        n1, n2 = phase_counts(counts, rng.choice([1, 8]), rng.randint(1, 40))
+        n1, n2 = phase_counts(counts, rng.choice([1, 8]), rng.randint(1, 40), rng.random() < 0.5)
         check_cover(n1, n2, rng.choice([8, 16, 24, 64, 256]), rng.random() < 0.5)
+
+
+def test_balanced_row_tiles_cover_each_expert_once():
+    """Balanced phase-1 tiles: ceil(rows/256) tiles of one height, a multiple of
+    32 between 160 and 256 (the row variants that exist) when there are two or
+    more, none empty, together covering the expert's rows exactly once; the
+    tile count per expert is the plain rule's."""
+    for span in range(1, 12000):
+        plain_tiles = -(-span // 256)
+        mf, h = phase_tiles(span, True)
+        if span <= 128:
+            assert mf == 0
+            continue
+        assert mf == plain_tiles
+        assert h % 32 == 0 and h <= 256 and (mf == 1 or h >= 160)
+        rows = [r for m in range(mf) for r in range(m * h, min((m + 1) * h, span))]
+        assert rows == list(range(span)), span
+        assert (mf - 1) * h < span, f"empty last tile at {span} rows"
 
 
 def test_grid_sizes_used_on_the_gpu_cover_each_path():
@@ -156,7 +189,7 @@ def test_grid_sizes_used_on_the_gpu_cover_each_path():
     reached = set()
     for counts, alignment, n, k, swiglu, grids in SCHEDULE_CASES:
         n_tiles = -(-n // (128 if swiglu else 256))
-        n1, n2 = phase_counts(counts, alignment, n_tiles)
+        n1, n2 = phase_counts(counts, alignment, n_tiles, balanced_for(swiglu, k))
         for grid in grids:
             pl, runs = check_cover(n1, n2, grid, not swiglu)
             per_q = {}
@@ -180,7 +213,8 @@ def test_grid_sizes_used_on_the_gpu_cover_each_path():
 
 
 def test_phase2_slots_rotate_over_the_cus():
-    # 14 rounds of 30 phase-1 columns per XCD: each workgroup carries short tiles in at most one round.
+    # Plain row tiles, 14 rounds of 30 phase-1 columns per XCD: each workgroup
+    # carries short tiles in at most one round.
     c4 = [1040, 1095, 1010, 1026, 1019, 1025, 1003, 974]
     pl, runs = check_cover(*phase_counts(c4, 8, 112), 256, False)
     rounds_carrying = [len({q for q, s in seq if s[0] == 1}) for seq in runs]
@@ -188,9 +222,17 @@ def test_phase2_slots_rotate_over_the_cus():
 
 
 def test_measured_shapes_get_the_intended_plans():
-    # H=4096, I=14336, E=8, 4096 tokens (counts from the bench): 14 rounds of phase 1
-    # alone would leave 448 short tiles for the end; one more round carries them all.
+    # H=4096, I=14336, E=8, 4096 tokens (counts from the bench). Gate/up GEMM
+    # (K=4096: balanced row tiles): the four experts of 1032-1096 rows get five
+    # 224-row tiles each, the others four of 256; no short tiles, so phase 1
+    # runs alone: 4032 tiles, 15.75 rounds.
     c4 = [1040, 1095, 1010, 1026, 1019, 1025, 1003, 974]
+    assert [phase_tiles(-(-c // 8) * 8, True) for c in c4] == [(5, 224), (5, 224), (4, 256), (5, 224), (4, 256),
+                                                               (5, 224), (4, 256), (4, 256)]
+    pl = ring_plan(*phase_counts(c4, 8, 112, balanced_for(True, 4096)), 256, False)
+    assert (pl["rounds"], pl["n2"], pl["rest"]["blocks"]) == (0, 0, 4032)
+    # With plain row tiles, 14 rounds of phase 1 alone would leave 448 short
+    # tiles for the end; one more round carries them all.
     pl = ring_plan(*phase_counts(c4, 8, 112), 256, False)
     assert (pl["rounds"], pl["cpr"], pl["carried"], pl["n2"]) == (15, 30, 448, 448)
     # Its down GEMM (512 full tiles = 2 rounds, 64 short tiles): no extra round;

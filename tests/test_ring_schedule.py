@@ -81,6 +81,7 @@ def _shapes():
     # Wide tiles: at most 4 stages in 160 KiB.
     shapes = {(tm, bnt, 160 * KIB, 4) for tm, bnt in itertools.product((64, 128, 256), (64, 128, 256))}
     shapes.add((32, 256, 160 * KIB, 4))  # short tiles of at most 32 rows
+    shapes |= {(tm, 256, 160 * KIB, 4) for tm in (160, 192, 224)}  # balanced row tiles
     # Decode tiles (grouped_gemm_decode_kernel): at most 8 stages in 160 KiB.
     for max_rows, bnt in ((64, 32), (128, 64), (128, 128)):  # down at 64 and 128 rows, gate/up at 128
         shapes |= {(64, bnt, 160 * KIB, 8), (max_rows, bnt, 160 * KIB, 8)}
@@ -187,8 +188,8 @@ def replay_chain(tm, bnt, lds, k_steps, tiles=3, cap=4):
     return sa, sb
 
 
-@pytest.mark.parametrize("tm,bnt", [(256, 256), (128, 256), (64, 256), (32, 256), (256, 128), (128, 128), (64, 128),
-                                    (256, 64), (128, 64), (64, 64)])
+@pytest.mark.parametrize("tm,bnt", [(256, 256), (224, 256), (192, 256), (160, 256), (128, 256), (64, 256), (32, 256),
+                                    (256, 128), (128, 128), (64, 128), (256, 64), (128, 64), (64, 64)])
 def test_chained_tiles_find_their_stages(tm, bnt):
     for k_steps in (4, 5, 7, 16, 64, 65):
         replay_chain(tm, bnt, 160 * KIB, k_steps)
