@@ -5,8 +5,8 @@
 // the caller passes; everything else (inputs, outputs, validation, kernels)
 // is moe_dispatch's.
 //
-// The dispatch plan sizes chunks so that chunks * experts <= 1024 for every
-// valid shape (dispatch.hip, plan_dispatch), so 1024 int32 counters always
+// The dispatch plan sizes chunks so that chunks * experts <= 4096 for every
+// valid shape (dispatch.hip, plan_dispatch), so 4096 int32 counters always
 // suffice. count_rank_kernel writes every counter a call reads, so nothing
 // needs clearing between calls. Each GPU holds one copy of the array for the
 // life of the process, and every call on that GPU uses it: calls on one GPU
@@ -17,7 +17,7 @@
 
 namespace moe {
 
-constexpr int64_t kStaticScratchBytes = 4096;
+constexpr int64_t kStaticScratchBytes = 16384;
 
 // The static scratch array. In host code its name is a host-side stand-in, not
 // a device address: it is never passed to a kernel or a copy. The device

@@ -162,7 +162,7 @@ int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, 
  * moe_dispatch with no scratch argument, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). No counterpart in the reference. It allocates
- * nothing: the kernels' per-chunk count table (at most 4096 bytes for every
+ * nothing: the kernels' per-chunk count table (at most 16384 bytes for every
  * valid shape; larger needs return MOE_ERR_WORKSPACE) lives in a static device
  * array of the library, one per GPU, kept until the process ends. Every call
  * on one GPU uses that GPU's array, so calls that overlap in time on one GPU
