@@ -137,26 +137,11 @@ def time_stages(block, x, steps, warmup):
     (every stage is idempotent given the previous stage's outputs)."""
     import torch
 
-    from moe_dispatch._extension import current_stream_handle
-
     with torch.inference_mode():
         block(x)  # a validated forward binds the launches; the next ones reuse them
         launches = block._launches[(x.shape[0], x.device)]
         assert launches.still_valid(block)
-        lib, bound, x_ptr = launches.lib, launches, x.data_ptr()
-
-        def call(name, *args):
-            lib.check(getattr(lib, name)(*args, current_stream_handle(bound.device_index)), name)
-
-        router_fn = "moe_router_fused_ranked" if bound.ranked else "moe_router_fused"
-        dispatch_fn = "moe_dispatch_ranked" if bound.ranked else "moe_dispatch"
-        stages = {
-            "router": lambda: call(router_fn, x_ptr, None, *bound.router),
-            "dispatch": lambda: call(dispatch_fn, x_ptr, *bound.dispatch),
-            "gateup_swiglu": lambda: call("moe_grouped_gateup_swiglu", *bound.gateup),
-            "down": lambda: call("moe_grouped_gemm", *bound.down),
-            "combine": lambda: call("moe_combine", *bound.combine),
-        }
+        stages = launches.stage_calls(x)
         return {name: {"mean_us": time_graph(fn, steps, warmup)} for name, fn in stages.items()}
 
 

@@ -30,6 +30,10 @@ int launch_grouped_gemm(const uint16_t*, const uint16_t*, uint16_t*, const int32
                         int64_t, int64_t, int, hipStream_t);
 int launch_gateup_swiglu(const uint16_t*, const uint16_t*, uint16_t*, const int32_t*, int64_t,
                          int64_t, int64_t, int, hipStream_t);
+int launch_gateup_swiglu_gathered(const uint16_t*, const int32_t*, int64_t, const uint16_t*, uint16_t*,
+                                  const int32_t*, int64_t, int64_t, int64_t, int, hipStream_t);
+int launch_dispatch_rows(const int32_t*, int32_t*, int32_t*, int32_t*, int32_t*, int32_t*, const int32_t*, int32_t*,
+                         int64_t, int64_t, int, int, int, int64_t, hipStream_t);
 void set_gemm_workgroup_limit(int);
 
 static thread_local char g_last_error[512] = "";
@@ -288,6 +292,69 @@ int moe_dispatch_ranked(const void* x, int dtype, const int32_t* ids, int32_t* c
                                   vectorized != 0, static_cast<hipStream_t>(stream));
 }
 
+// The checks of the row-table dispatch entry points (no x, no packed rows).
+static int check_dispatch_rows(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* slots,
+                               int32_t* inverse, int32_t* row_src, const void* table, int64_t tokens,
+                               int64_t experts, int64_t topk, int64_t alignment, int64_t packed_rows) {
+    MOE_REQUIRE(tokens >= 0, MOE_ERR_INVALID_ARGUMENT, "incompatible token dimensions");
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
+    MOE_REQUIRE(topk >= 1 && topk <= kMaxTopk, MOE_ERR_UNSUPPORTED, "topk must be in 1..8");
+    MOE_REQUIRE(alignment >= 1 && alignment <= 128, MOE_ERR_INVALID_ARGUMENT, "alignment must be 1..128");
+    const int64_t n = tokens * topk;
+    const int64_t required = aligned_capacity(n, experts, alignment);
+    MOE_REQUIRE(n <= INT_MAX && required <= INT_MAX, MOE_ERR_CAPACITY, "shape exceeds int32 indexing capacity");
+    MOE_REQUIRE(packed_rows >= required, MOE_ERR_WORKSPACE, "row table has %lld rows, needs %lld",
+                (long long)packed_rows, (long long)required);
+    MOE_REQUIRE(counts && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(n == 0 || (ids && slots && inverse && row_src), MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(aligned_to(ids, 4) && aligned_to(counts, 4) && aligned_to(offsets, 4) && aligned_to(slots, 4) &&
+                    aligned_to(inverse, 4) && aligned_to(row_src, 4) && aligned_to(table, 4),
+                MOE_ERR_INVALID_ARGUMENT, "index buffers must be 4-byte aligned");
+    return MOE_OK;
+}
+
+int moe_dispatch_rows(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* slots, int32_t* inverse,
+                      int32_t* row_src, void* scratch, int64_t scratch_bytes, int64_t tokens, int64_t experts,
+                      int64_t topk, int64_t alignment, int64_t packed_rows, void* stream) {
+    const int rc = check_dispatch_rows(ids, counts, offsets, slots, inverse, row_src, scratch, tokens, experts,
+                                       topk, alignment, packed_rows);
+    if (rc != MOE_OK) return rc;
+    const int64_t need = dispatch_scratch_bytes(tokens, experts, topk);
+    MOE_REQUIRE(scratch_bytes >= need, MOE_ERR_WORKSPACE, "dispatch scratch has %lld bytes, needs %lld",
+                (long long)scratch_bytes, (long long)need);
+    MOE_REQUIRE(scratch, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    return launch_dispatch_rows(ids, counts, offsets, slots, inverse, row_src, nullptr, static_cast<int32_t*>(scratch),
+                                0, tokens, (int)experts, (int)topk, (int)alignment, packed_rows,
+                                static_cast<hipStream_t>(stream));
+}
+
+int moe_dispatch_ranked_rows(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* slots,
+                             int32_t* inverse, int32_t* row_src, const int32_t* ranks, const int32_t* tile_counts,
+                             int64_t tile_counts_bytes, int64_t tile_tokens, int64_t tokens, int64_t experts,
+                             int64_t topk, int64_t alignment, int64_t packed_rows, void* stream) {
+    const int rc = check_dispatch_rows(ids, counts, offsets, slots, inverse, row_src, tile_counts, tokens, experts,
+                                       topk, alignment, packed_rows);
+    if (rc != MOE_OK) return rc;
+    const int64_t tile = router_rank_tile(tokens, experts);
+    MOE_REQUIRE(tokens == 0 || (tile > 0 && tile_tokens == tile), MOE_ERR_INVALID_ARGUMENT,
+                "tile_tokens %lld is not the ranked route's tile (%lld) for this shape", (long long)tile_tokens,
+                (long long)tile);
+    if (tokens > 0) {
+        const int64_t need = (tokens + tile - 1) / tile * experts * 4;
+        MOE_REQUIRE(tile_counts_bytes >= need, MOE_ERR_WORKSPACE, "tile counts need %lld bytes, got %lld",
+                    (long long)need, (long long)tile_counts_bytes);
+        MOE_REQUIRE(ranks && tile_counts, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    }
+    MOE_REQUIRE(aligned_to(ranks, 4), MOE_ERR_INVALID_ARGUMENT, "index buffers must be 4-byte aligned");
+    if (tokens == 0)  // no assignments: counts and offsets are zero (the count-in-pack path reads no table)
+        return launch_dispatch_rows(ids, counts, offsets, slots, inverse, row_src, nullptr, nullptr, 0, tokens,
+                                    (int)experts, (int)topk, (int)alignment, packed_rows,
+                                    static_cast<hipStream_t>(stream));
+    return launch_dispatch_rows(ids, counts, offsets, slots, inverse, row_src, ranks,
+                                const_cast<int32_t*>(tile_counts), tile, tokens, (int)experts, (int)topk,
+                                (int)alignment, packed_rows, static_cast<hipStream_t>(stream));
+}
+
 int moe_combine(const void* expert_output, int dtype, const int32_t* inverse,
                 const float* weights, void* output, int64_t tokens, int64_t hidden,
                 int64_t topk, int64_t packed_rows, void* stream) {
@@ -360,6 +427,29 @@ int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
                                 static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(act),
                                 offsets, rows, hidden, intermediate, (int)experts,
                                 static_cast<hipStream_t>(stream));
+}
+
+int moe_grouped_gateup_swiglu_gathered(const void* x, const int32_t* row_src, int64_t x_rows, const void* gate_up,
+                                       void* act, const int32_t* offsets, int64_t rows, int64_t hidden,
+                                       int64_t intermediate, int64_t experts, void* stream) {
+    MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
+    MOE_REQUIRE(rows >= 0 && rows <= INT_MAX && x_rows >= 0 && x_rows <= INT_MAX, MOE_ERR_CAPACITY,
+                "rows exceed int32");
+    MOE_REQUIRE(hidden > 0 && intermediate > 0 && hidden % 64 == 0 && intermediate % 8 == 0, MOE_ERR_UNSUPPORTED,
+                "gathered gate/up needs hidden a positive multiple of 64 and intermediate of 8");
+    MOE_REQUIRE(hidden <= INT_MAX && intermediate <= INT_MAX && 2 * intermediate * hidden * 2 <= UINT32_MAX &&
+                    256 * hidden * 2 <= UINT32_MAX,
+                MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
+    // x is one buffer of 32-bit offsets, with 2 GiB and up left for the out-of-range marker.
+    MOE_REQUIRE(x_rows * hidden * 2 < (int64_t{1} << 31), MOE_ERR_CAPACITY, "x must be below 2 GiB");
+    if (rows == 0) return MOE_OK;
+    MOE_REQUIRE(x && row_src && gate_up && act && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
+    MOE_REQUIRE(aligned_to(x, 16) && aligned_to(gate_up, 16) && aligned_to(act, 16) && aligned_to(offsets, 4) &&
+                    aligned_to(row_src, 4),
+                MOE_ERR_INVALID_ARGUMENT, "x, gate_up and act must be 16-byte aligned (index buffers 4-byte)");
+    return launch_gateup_swiglu_gathered(static_cast<const uint16_t*>(x), row_src, x_rows,
+                                         static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(act), offsets,
+                                         rows, hidden, intermediate, (int)experts, static_cast<hipStream_t>(stream));
 }
 
 int moe_set_gemm_workgroups(int64_t workgroups) {

@@ -124,12 +124,15 @@ constexpr int kSmallAssign = 1024;
 // into slots itself, a ranked route into a buffer of its own. Destination and
 // padding rows are kept below packed_rows (they are for consistent counts and
 // ranks; a caller's inconsistent pair is not written out of bounds).
-template <int VB, bool COUNT>
+// ROWS: the layout without the rows. Instead of copying x rows into packed,
+// row_src[r] receives the token whose row packed row r would hold (-1 for
+// padding rows), for a GEMM that reads its A rows from x through it.
+template <int VB, bool COUNT, bool ROWS>
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const char* __restrict__ x, const int32_t* __restrict__ ids, int32_t* slots,
     const int32_t* ranks, const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, char* __restrict__ packed, int32_t* __restrict__ inverse,
-    int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
+    int32_t* __restrict__ row_src, int64_t tokens, int64_t row_bytes, int experts, int topk, int alignment,
     int64_t chunk_tokens, int pack_tokens, int n_chunks, int experts_pow2, int64_t packed_rows) {
     using V = typename VecOf<VB>::T;
     __shared__ int part_all[kPackThreads / kWave][kMaxExperts];
@@ -156,10 +159,12 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
         return reinterpret_cast<const V*>(x + (t0 + tl) * row_bytes)[i - tl * nv];
     };
     V early[kPackEarly];
+    if constexpr (!ROWS) {
 #pragma unroll
-    for (int j = 0; j < kPackEarly; ++j) {
-        const int i = tid + j * kPackThreads;
-        if (i < items) early[j] = src(i);
+        for (int j = 0; j < kPackEarly; ++j) {
+            const int i = tid + j * kPackThreads;
+            if (i < items) early[j] = src(i);
+        }
     }
     // This thread's assignment (n_tok * K <= kPackMaxAssign == kPackThreads):
     // its expert and in-chunk rank do not depend on the prefix either.
@@ -294,6 +299,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
                 d = row;
                 slots[my_p] = static_cast<int32_t>(slot);
                 inverse[my_p] = static_cast<int32_t>(d);
+                if constexpr (ROWS) row_src[d] = static_cast<int32_t>(t0 + tid / topk);
             }
         } else {
             slots[my_p] = -1;  // out-of-range id (the count/rank pass also writes -1)
@@ -311,20 +317,26 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
             if (d >= 0) reinterpret_cast<V*>(packed + d * row_bytes)[v] = val;
         }
     };
+    if constexpr (!ROWS) {
 #pragma unroll
-    for (int j = 0; j < kPackEarly; ++j) {
-        const int i = tid + j * kPackThreads;
-        if (i < items) store(i, early[j]);
+        for (int j = 0; j < kPackEarly; ++j) {
+            const int i = tid + j * kPackThreads;
+            if (i < items) store(i, early[j]);
+        }
+        for (int i = tid + kPackEarly * kPackThreads; i < items; i += kPackThreads) store(i, src(i));
     }
-    for (int i = tid + kPackEarly * kPackThreads; i < items; i += kPackThreads) store(i, src(i));
 
-    // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero.
+    // (d) Padding rows [offs[e] + total[e], offs[e+1]) are zero (ROWS: map to -1).
     for (int e = blockIdx.x; e < experts; e += gridDim.x) {
         const int64_t r0 = max(static_cast<int64_t>(offs[e]) + total[e], static_cast<int64_t>(0));
         const int64_t r1 = min(static_cast<int64_t>(offs[e + 1]), packed_rows);
-        const int64_t pad_items = (r1 - r0) * nv;
-        V* base = reinterpret_cast<V*>(packed + r0 * row_bytes);
-        for (int64_t i = tid; i < pad_items; i += kPackThreads) base[i] = zero_vec<V>();
+        if constexpr (ROWS) {
+            for (int64_t r = r0 + tid; r < r1; r += kPackThreads) row_src[r] = -1;
+        } else {
+            const int64_t pad_items = (r1 - r0) * nv;
+            V* base = reinterpret_cast<V*>(packed + r0 * row_bytes);
+            for (int64_t i = tid; i < pad_items; i += kPackThreads) base[i] = zero_vec<V>();
+        }
     }
 }
 
@@ -476,7 +488,7 @@ static int launch_pack(const void* x, int dtype, const int32_t* ids, int32_t* co
                        int32_t* slots, const int32_t* ranks, void* packed, int32_t* inverse,
                        const int32_t* chunk_counts, int64_t tokens, int64_t hidden, int experts, int topk,
                        int alignment, int64_t packed_rows, bool vectorized, const DispatchPlan& plan,
-                       bool count_in_pack, hipStream_t stream);
+                       bool count_in_pack, hipStream_t stream, int32_t* row_src = nullptr);
 
 int launch_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts,
                     int32_t* offsets, int32_t* slots, void* packed, int32_t* inverse,
@@ -512,11 +524,50 @@ int launch_dispatch_ranked(const void* x, int dtype, const int32_t* ids, int32_t
                        hidden, experts, topk, alignment, packed_rows, vectorized, plan, false, stream);
 }
 
+// The layout without the rows: counts, offsets, slots and inverse as
+// launch_dispatch writes them, and row_src (packed_rows int32) the token of
+// each packed row (-1 for padding; rows >= offsets[E] untouched). With
+// `ranks` (a ranked route's tiles of tile_tokens tokens) the pack kernel
+// alone; otherwise the counting kernel first, into chunk_counts.
+int launch_dispatch_rows(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* slots, int32_t* inverse,
+                         int32_t* row_src, const int32_t* ranks, int32_t* chunk_counts, int64_t tile_tokens,
+                         int64_t tokens, int experts, int topk, int alignment, int64_t packed_rows,
+                         hipStream_t stream) {
+    // 16-byte "rows": a block takes as many tokens as its assignment budget allows.
+    const DispatchPlan plan = plan_dispatch(tokens, experts, topk, 16, ranks ? tile_tokens : 0);
+    const int64_t n_assign = tokens * topk;
+    const bool count_in_pack = ranks == nullptr && n_assign <= kSmallAssign;
+    if (ranks == nullptr && plan.n_chunks > 0 && !count_in_pack) {
+        hipLaunchKernelGGL(count_rank_kernel, dim3(static_cast<unsigned>(plan.n_chunks)), dim3(kRankThreads), 0,
+                           stream, ids, slots, chunk_counts, n_assign, experts, plan.chunk_tokens * topk);
+        const int rc = check_launch("count_rank_kernel");
+        if (rc != MOE_OK) return rc;
+    }
+    return launch_pack(nullptr, 0, ids, counts, offsets, slots, ranks ? ranks : slots, nullptr, inverse,
+                       chunk_counts, tokens, 0, experts, topk, alignment, packed_rows, false, plan, count_in_pack,
+                       stream, row_src);
+}
+
 static int launch_pack(const void* x, int dtype, const int32_t* ids, int32_t* counts, int32_t* offsets,
                        int32_t* slots, const int32_t* ranks, void* packed, int32_t* inverse,
                        const int32_t* chunk_counts, int64_t tokens, int64_t hidden, int experts, int topk,
                        int alignment, int64_t packed_rows, bool vectorized, const DispatchPlan& plan,
-                       bool count_in_pack, hipStream_t stream) {
+                       bool count_in_pack, hipStream_t stream, int32_t* row_src) {
+    const int experts_pow2_rows = static_cast<int>(pow2_at_least(experts));
+    if (row_src != nullptr) {  // the row table instead of the rows (x and packed unused)
+#define MOE_ROWS_LAUNCH(CNT)                                                                             \
+    hipLaunchKernelGGL((pack_kernel<16, CNT, true>), dim3(static_cast<unsigned>(plan.pack_blocks)),       \
+                       dim3(kPackThreads), 0, stream, nullptr, ids, slots, ranks, chunk_counts, counts,    \
+                       offsets, nullptr, inverse, row_src, tokens, int64_t{16}, experts, topk, alignment, \
+                       plan.chunk_tokens, plan.pack_tokens, static_cast<int>(plan.n_chunks),              \
+                       experts_pow2_rows, packed_rows)
+        if (count_in_pack)
+            MOE_ROWS_LAUNCH(true);
+        else
+            MOE_ROWS_LAUNCH(false);
+#undef MOE_ROWS_LAUNCH
+        return check_launch("pack_kernel");
+    }
     const int64_t elem = dtype_size(dtype);
     const int64_t row_bytes = hidden * elem;
     // The widest access that divides the row size and both base addresses (an
@@ -537,9 +588,9 @@ static int launch_pack(const void* x, int dtype, const int32_t* ids, int32_t* co
     const int experts_pow2 = static_cast<int>(pow2_at_least(experts));
     const dim3 grid(static_cast<unsigned>(plan.pack_blocks));
 #define MOE_PACK_LAUNCH(VBV, CNT)                                                              \
-    hipLaunchKernelGGL((pack_kernel<VBV, CNT>), grid, dim3(kPackThreads), 0, stream,            \
+    hipLaunchKernelGGL((pack_kernel<VBV, CNT, false>), grid, dim3(kPackThreads), 0, stream,     \
                        static_cast<const char*>(x), ids, slots, ranks, chunk_counts, counts, offsets, \
-                       static_cast<char*>(packed), inverse, tokens, row_bytes, experts, topk,    \
+                       static_cast<char*>(packed), inverse, nullptr, tokens, row_bytes, experts, topk, \
                        alignment, plan.chunk_tokens, plan.pack_tokens,                          \
                        static_cast<int>(plan.n_chunks), experts_pow2, packed_rows)
 #define MOE_PACK_CASE(VBV)                 \

@@ -43,7 +43,7 @@ constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;  // k-step: one 128-byte LDS row
 
 struct GemmParams {
-    const uint16_t* a;        // [R, K]
+    const uint16_t* a;        // [R, K], or with a_rows the [a_src_rows, K] rows they index
     const uint16_t* b;        // [E, NB, K]  (NB = N, or 2I for gate/up)
     uint16_t* c;              // [R, ldc]
     const int32_t* offsets;   // [E + 1]
@@ -54,7 +54,15 @@ struct GemmParams {
     int64_t rows;             // rows of A and C; spans are clamped to it
     int experts;
     int n_tiles;              // output column tiles
+    // Gathered A (gate/up GEMM of the ring kernels only): row r of the
+    // product reads row a_rows[r] of `a` (zero when negative); null: row r.
+    const int32_t* a_rows;
+    int64_t a_src_rows;
 };
+
+// A buffer offset past every buffer's range (buffers hold at most 2 GiB): the
+// load returns zero and moves no data.
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 // 16-byte chunk c of LDS row r lives at physical chunk c ^ f(r), f(r) = (r ^ (r >> 3)) & 7.
 // A 16-byte read is serviced 16 lanes at a time across 64 four-byte banks (two
@@ -334,8 +342,9 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // row0 + TMR) of one expert (clamped to row_end) by BNT weight rows from
 // output column col0, in the first LDS_BYTES of `lds`, at most MAXS stages
 // deep. The four waves split the tile as (4/WC) row blocks x WC column blocks.
-template <int TMR, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2, int MAXS = 4>
+template <int TMR, int BNT, bool SWIGLU, uint32_t LDS_BYTES, int WC = 2, int MAXS = 4, bool GATHER = false>
 struct RingOps {
+    static_assert(!GATHER || SWIGLU, "only the gate/up GEMM gathers its rows");
     static constexpr int WAVES = kRingThreads / kWave;
     static constexpr int TM = TMR;
     static constexpr int WTM = TM / (WAVES / WC);  // the four waves as (4/WC) x WC
@@ -368,38 +377,68 @@ struct RingOps {
     char* lds;
     int wave;
 
-    // A tile's two buffer resources: its rows of A, and the expert's weight rows
-    // from the tile's first column on (so the per-lane offsets below do not
-    // depend on the tile). Rows past the tile (or the expert) read as zero.
+    // A tile's two buffer resources and its per-lane A offsets. B: the
+    // expert's weight rows from the tile's first column on (so the per-lane B
+    // offsets below do not depend on the tile). A: the tile's rows of A, read
+    // at offsets relative to its first row; or, gathered (gate/up with
+    // a_rows), the whole source at each row's own offset. Rows past the tile
+    // (or the expert), and gathered rows mapped to a negative index, read as
+    // zero (out of the buffer's range). Load l of a stage covers LDS rows
+    // (wave * X_LOADS + l) * 8 + lane / 8.
     struct Rsrc {
         __amdgpu_buffer_rsrc_t a, b;
+        uint32_t a_off[A_LOADS];
     };
+    // GATHER with `offsets` false leaves a_off to the caller (its table loads
+    // belong where the tile's prologue is issued, see ring_tile's a_carry).
     static __device__ __forceinline__ Rsrc tile_rsrc(const GemmParams& p, int expert, int64_t col0, int64_t row0,
-                                                     int64_t row_end) {
+                                                     int64_t row_end, bool offsets = true) {
         const int64_t K = p.k;
-        const int64_t a_rows = min<int64_t>(row_end - row0, TM);
-        return Rsrc{make_rsrc(p.a + row0 * K, static_cast<uint32_t>(a_rows * K * 2)),
-                    make_rsrc(p.b + (static_cast<int64_t>(expert) * p.nb + col0) * K,
-                              static_cast<uint32_t>((p.nb - col0) * K * 2))};
+        const int lane = threadIdx.x & 63;
+        const int wave_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int lrow = lane >> 3;
+        const int pchunk = lane & 7;
+        Rsrc r;
+        r.b = make_rsrc(p.b + (static_cast<int64_t>(expert) * p.nb + col0) * K,
+                        static_cast<uint32_t>((p.nb - col0) * K * 2));
+        if constexpr (GATHER) {
+            r.a = make_rsrc(p.a, static_cast<uint32_t>(p.a_src_rows * K * 2));
+            if (!offsets) return r;
+#pragma unroll
+            for (int i = 0; i < A_LOADS; ++i) {
+                const int rr = (wave_ * A_LOADS + i) * 8 + lrow;
+                const int src = row0 + rr < row_end ? p.a_rows[row0 + rr] : -1;
+                r.a_off[i] = src >= 0 && src < p.a_src_rows
+                                 ? static_cast<uint32_t>((src * K + (pchunk ^ ring_key(rr)) * 8) * 2)
+                                 : kOutOfRange;
+            }
+        } else {
+            const int64_t a_rows = min<int64_t>(row_end - row0, TM);
+            r.a = make_rsrc(p.a + row0 * K, static_cast<uint32_t>(a_rows * K * 2));
+#pragma unroll
+            for (int i = 0; i < A_LOADS; ++i) {
+                const int rr = (wave_ * A_LOADS + i) * 8 + lrow;
+                r.a_off[i] = static_cast<uint32_t>((rr * K + (pchunk ^ ring_key(rr)) * 8) * 2);
+            }
+        }
+        return r;
     }
 
     __device__ __forceinline__ RingOps(const GemmParams& p, char* lds_, int expert, int64_t col0,
                                        int64_t row0, int64_t row_end)
-        : lds(lds_) {
+        : RingOps(p, lds_, tile_rsrc(p, expert, col0, row0, row_end)) {}
+
+    // From a tile's resources already formed (a chained next tile's).
+    __device__ __forceinline__ RingOps(const GemmParams& p, char* lds_, const Rsrc& r) : lds(lds_) {
         const int lane = threadIdx.x & 63;
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int64_t K = p.k;
-        const Rsrc r = tile_rsrc(p, expert, col0, row0, row_end);
         rsrc_a = r.a;
         rsrc_b = r.b;
-        // Load l of a stage covers LDS rows (wave * X_LOADS + l) * 8 + lane / 8.
         const int lrow = lane >> 3;
         const int pchunk = lane & 7;
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-        const int r = (wave * A_LOADS + i) * 8 + lrow;
-        a_off[i] = static_cast<uint32_t>((r * K + (pchunk ^ ring_key(r)) * 8) * 2);
-    }
+    for (int i = 0; i < A_LOADS; ++i) a_off[i] = r.a_off[i];
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
         const int r = (wave * B_LOADS + i) * 8 + lrow;
@@ -419,10 +458,10 @@ struct RingOps {
     }
     // Load l of stage kt into ring slot st, of A and of B (of this tile, or of
     // the tile whose resources are given).
-    __device__ __forceinline__ void issue_a(int kt, int st, int l) const { issue_a(rsrc_a, kt, st, l); }
+    __device__ __forceinline__ void issue_a(int kt, int st, int l) const { issue_a(rsrc_a, kt, st, l, a_off[l]); }
     __device__ __forceinline__ void issue_b(int kt, int st, int l) const { issue_b(rsrc_b, kt, st, l); }
-    __device__ __forceinline__ void issue_a(__amdgpu_buffer_rsrc_t r, int kt, int st, int l) const {
-        dma16(r, lds + st * A_STAGE + (wave * A_LOADS + l) * 1024, a_off[l], static_cast<uint32_t>(kt) * kRowBytes);
+    __device__ __forceinline__ void issue_a(__amdgpu_buffer_rsrc_t r, int kt, int st, int l, uint32_t off) const {
+        dma16(r, lds + st * A_STAGE + (wave * A_LOADS + l) * 1024, off, static_cast<uint32_t>(kt) * kRowBytes);
     }
     __device__ __forceinline__ void issue_b(__amdgpu_buffer_rsrc_t r, int kt, int st, int l) const {
         dma16(r, lds + B_BASE + st * B_STAGE + (wave * B_LOADS + l) * 1024, b_off[l],
@@ -476,13 +515,15 @@ struct NoHook {
 // tile of the same shape and k) into the slots that follow, so the next tile
 // starts at slots (sa0 + k_steps) % SA and (sb0 + k_steps) % SB and its hook
 // only issues the prologue's last window. Requires k_steps >= SB.
-template <int TMR, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4>
+template <int TMR, int BNT, bool SWIGLU, uint32_t LDS_BYTES, typename Hook = NoHook, int WC = 2, int MAXS = 4,
+          bool GATHER = false>
 __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int expert, int64_t col0,
                                           int64_t row0, int64_t row_end, bool own_prologue = true,
                                           bool wait_all = false, const Hook& hook = Hook{}, int sa0 = 0, int sb0 = 0,
                                           bool chain = false,
-                                          typename RingOps<TMR, BNT, SWIGLU, LDS_BYTES, WC, MAXS>::Rsrc next = {}) {
-    using R = RingOps<TMR, BNT, SWIGLU, LDS_BYTES, WC, MAXS>;
+                                          typename RingOps<TMR, BNT, SWIGLU, LDS_BYTES, WC, MAXS, GATHER>::Rsrc next = {},
+                                          const uint32_t* a_carry = nullptr) {
+    using R = RingOps<TMR, BNT, SWIGLU, LDS_BYTES, WC, MAXS, GATHER>;
     constexpr int WTM = R::WTM, WTN = R::WTN, FA = R::FA, FB = R::FB;
     constexpr int A_LOADS = R::A_LOADS, B_LOADS = R::B_LOADS;
     constexpr int SA = R::SA, SB = R::SB;
@@ -493,7 +534,15 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     const int wm = wave / WC;
     const int wn = wave % WC;
     const int64_t K = p.k;
-    const R ops(p, lds, expert, col0, row0, row_end);
+    // Gathered rows: the tile's A offsets were formed where its prologue was
+    // issued (a_carry). Forming them here would load the row table after the
+    // ring's loads, and the first refill's wait for it would drain the ring.
+    typename R::Rsrc cur = R::tile_rsrc(p, expert, col0, row0, row_end, !GATHER);
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int i = 0; i < R::A_LOADS; ++i) cur.a_off[i] = a_carry[i];
+    }
+    const R ops(p, lds, cur);
 
     // Per-lane fragment addresses: lane l reads row (l%16) of a fragment at k
     // chunk l/16 of the sub-step (all 32 k of it in one 16-byte read). Fragments
@@ -558,13 +607,15 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     struct Refill {
         int kt_a, slot_a, kt_b, slot_b;
         __amdgpu_buffer_rsrc_t ra, rb;  // this tile's or (chained) the next tile's
+        bool a_next;                    // A loads of the next tile (its own offsets when gathered)
     };
     auto refill_at = [&](auto g_c, const Refill& r) {
         constexpr int g = decltype(g_c)::value;  // MFMA slot in the window
         static_for<A_LOADS>([&](auto l_c) {
             constexpr int l = decltype(l_c)::value;
             constexpr int slot = kQuarters ? l * HM / A_LOADS : l * 4 * HM / LOADS;
-            if constexpr (slot == g) ops.issue_a(r.ra, r.kt_a, r.slot_a, l);
+            if constexpr (slot == g)
+                ops.issue_a(r.ra, r.kt_a, r.slot_a, l, GATHER && r.a_next ? next.a_off[l] : ops.a_off[l]);
         });
         static_for<B_LOADS>([&](auto l_c) {
             constexpr int l = decltype(l_c)::value;
@@ -633,7 +684,7 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     // stage u+1; this window refills the slots stage u just freed.
     using NoLoads = std::integral_constant<int, -1>;
     using More = std::false_type;
-    const Refill none{0, 0, 0, 0, ops.rsrc_a, ops.rsrc_b};
+    const Refill none{0, 0, 0, 0, ops.rsrc_a, ops.rsrc_b, false};
     first_half(vb[0] + b_first, NoLoads{}, none);
     second_half(va[1] + a_first, vb[1] + b_first, More{}, NoLoads{}, none);
     first_half(vb[1] + b_first, NoLoads{}, none);
@@ -647,7 +698,7 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         const bool b_next = chain && u + SB >= k_steps;
         const Refill rf{a_next ? u + SA - k_steps : min(u + SA, k_steps - 1), sa,
                         b_next ? u + SB - k_steps : min(u + SB, k_steps - 1), sb,
-                        a_next ? next.a : ops.rsrc_a, b_next ? next.b : ops.rsrc_b};
+                        a_next ? next.a : ops.rsrc_a, b_next ? next.b : ops.rsrc_b, a_next};
         const uint32_t a0 = va[0] + na * A_STAGE, a1 = va[1] + na * A_STAGE;
         const uint32_t b0 = vb[0] + nb * B_STAGE, b1 = vb[1] + nb * B_STAGE;
         fence();
@@ -994,18 +1045,25 @@ __device__ __forceinline__ RingWork ring_locate(const GemmParams& p, const RingT
     return w;
 }
 
-template <bool SWIGLU>
-__device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, const RingWork& w) {
+// Issues tile w's prologue; with GATHER also leaves its A offsets in a_carry.
+template <bool SWIGLU, bool GATHER>
+__device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, const RingWork& w, uint32_t* a_carry) {
     const int k_steps = static_cast<int>(p.k / kStageK);
-    auto go = [&](auto ops) { ops.prologue(k_steps); };
+    auto go = [&](auto ops) {
+        ops.prologue(k_steps);
+        if constexpr (GATHER) {
+#pragma unroll
+            for (int i = 0; i < decltype(ops)::A_LOADS; ++i) a_carry[i] = ops.a_off[i];
+        }
+    };
     switch (w.variant) {
-        case 0: go(RingOps<256, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 1: go(RingOps<128, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 2: go(RingOps<64, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 9: go(RingOps<32, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 10: go(RingOps<224, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 11: go(RingOps<192, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
-        case 12: go(RingOps<160, 256, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 0: go(RingOps<256, 256, SWIGLU, kRingBytes, 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 1: go(RingOps<128, 256, SWIGLU, kRingBytes, 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 2: go(RingOps<64, 256, SWIGLU, kRingBytes, 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 9: go(RingOps<32, 256, SWIGLU, kRingBytes, 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 10: go(RingOps<224, 256, SWIGLU, kRingBytes, 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 11: go(RingOps<192, 256, SWIGLU, kRingBytes, 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
+        case 12: go(RingOps<160, 256, SWIGLU, kRingBytes, 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end)); break;
         default:
             if constexpr (!SWIGLU) {
                 if (w.variant == 3) go(RingOps<256, 128, false, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end));
@@ -1023,10 +1081,11 @@ __device__ __forceinline__ void ring_prologue(const GemmParams& p, char* lds, co
 // enough, the two are chained (see ring_tile): `w`'s last windows load `nxt`'s
 // first stages and its hook issues only the prologue's last window. Otherwise
 // the hook issues `nxt`'s whole prologue at slots 0.
-template <int TMR, int BNT, bool SWIGLU>
+template <int TMR, int BNT, bool SWIGLU, bool GATHER = false>
 __device__ __forceinline__ void ring_run_shape(const GemmParams& p, char* lds, const RingWork& w,
-                                               const RingWork& nxt, bool wait_all, int& sa, int& sb) {
-    using R = RingOps<TMR, BNT, SWIGLU, kRingBytes>;
+                                               const RingWork& nxt, bool wait_all, int& sa, int& sb,
+                                               uint32_t* a_carry) {
+    using R = RingOps<TMR, BNT, SWIGLU, kRingBytes, 2, 4, GATHER>;
     const int k_steps = static_cast<int>(p.k / kStageK);
     // Wave-uniform (it selects buffer resources, which live in SGPRs).
     const bool chain = __builtin_amdgcn_readfirstlane(nxt.valid && nxt.variant == w.variant && k_steps >= R::SB) != 0;
@@ -1035,41 +1094,51 @@ __device__ __forceinline__ void ring_run_shape(const GemmParams& p, char* lds, c
     const int na = (sa + k_steps) % R::SA, nb = (sb + k_steps) % R::SB;
     auto hook = [&] {
         if (!nxt.valid) return;
-        if (chain)
-            R(p, lds, nxt.expert, nxt.col0, nxt.row0, nxt.row_end).prologue(k_steps, na, nb, true);
-        else
-            ring_prologue<SWIGLU>(p, lds, nxt);
+        if (chain) {
+            // Gathered rows: the next tile's offsets, formed before its k-loop;
+            // otherwise they do not depend on the tile.
+            if constexpr (GATHER) {
+                R(p, lds, next).prologue(k_steps, na, nb, true);
+#pragma unroll
+                for (int i = 0; i < R::A_LOADS; ++i) a_carry[i] = next.a_off[i];
+            } else {
+                R(p, lds, nxt.expert, nxt.col0, nxt.row0, nxt.row_end).prologue(k_steps, na, nb, true);
+            }
+        } else {
+            ring_prologue<SWIGLU, GATHER>(p, lds, nxt, a_carry);
+        }
     };
-    ring_tile<TMR, BNT, SWIGLU, kRingBytes>(p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook,
-                                             sa, sb, chain, next);
+    ring_tile<TMR, BNT, SWIGLU, kRingBytes, decltype(hook), 2, 4, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end,
+                                                                           false, wait_all, hook, sa, sb, chain, next,
+                                                                           a_carry);
     sa = chain ? na : 0;
     sb = chain ? nb : 0;
 }
 
-template <bool SWIGLU>
+template <bool SWIGLU, bool GATHER>
 __device__ __forceinline__ void ring_run(const GemmParams& p, char* lds, const RingWork& w, const RingWork& nxt,
-                                         bool wait_all, int& sa, int& sb) {
+                                         bool wait_all, int& sa, int& sb, uint32_t* a_carry) {
     switch (w.variant) {
-        case 0: ring_run_shape<256, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 1: ring_run_shape<128, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 2: ring_run_shape<64, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 9: ring_run_shape<32, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 10: ring_run_shape<224, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 11: ring_run_shape<192, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
-        case 12: ring_run_shape<160, 256, SWIGLU>(p, lds, w, nxt, wait_all, sa, sb); break;
+        case 0: ring_run_shape<256, 256, SWIGLU, GATHER>(p, lds, w, nxt, wait_all, sa, sb, a_carry); break;
+        case 1: ring_run_shape<128, 256, SWIGLU, GATHER>(p, lds, w, nxt, wait_all, sa, sb, a_carry); break;
+        case 2: ring_run_shape<64, 256, SWIGLU, GATHER>(p, lds, w, nxt, wait_all, sa, sb, a_carry); break;
+        case 9: ring_run_shape<32, 256, SWIGLU, GATHER>(p, lds, w, nxt, wait_all, sa, sb, a_carry); break;
+        case 10: ring_run_shape<224, 256, SWIGLU, GATHER>(p, lds, w, nxt, wait_all, sa, sb, a_carry); break;
+        case 11: ring_run_shape<192, 256, SWIGLU, GATHER>(p, lds, w, nxt, wait_all, sa, sb, a_carry); break;
+        case 12: ring_run_shape<160, 256, SWIGLU, GATHER>(p, lds, w, nxt, wait_all, sa, sb, a_carry); break;
         default:
             if constexpr (!SWIGLU) {
-                if (w.variant == 3) ring_run_shape<256, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 4) ring_run_shape<128, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 5) ring_run_shape<64, 128, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 6) ring_run_shape<256, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else if (w.variant == 7) ring_run_shape<128, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
-                else ring_run_shape<64, 64, false>(p, lds, w, nxt, wait_all, sa, sb);
+                if (w.variant == 3) ring_run_shape<256, 128, false>(p, lds, w, nxt, wait_all, sa, sb, a_carry);
+                else if (w.variant == 4) ring_run_shape<128, 128, false>(p, lds, w, nxt, wait_all, sa, sb, a_carry);
+                else if (w.variant == 5) ring_run_shape<64, 128, false>(p, lds, w, nxt, wait_all, sa, sb, a_carry);
+                else if (w.variant == 6) ring_run_shape<256, 64, false>(p, lds, w, nxt, wait_all, sa, sb, a_carry);
+                else if (w.variant == 7) ring_run_shape<128, 64, false>(p, lds, w, nxt, wait_all, sa, sb, a_carry);
+                else ring_run_shape<64, 64, false>(p, lds, w, nxt, wait_all, sa, sb, a_carry);
             }
     }
 }
 
-template <bool SWIGLU>
+template <bool SWIGLU, bool GATHER>
 __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) char lds[kRingBytes];
     // Balanced row tiles for the gate/up GEMM at K >= 2048. There a short last
@@ -1096,7 +1165,8 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
     int q = blockIdx.x, sub = 0;
     RingWork cur = next(q, sub);
     if (!cur.valid) return;
-    ring_prologue<SWIGLU>(p, lds, cur);
+    uint32_t a_carry[8];  // GATHER: the next tile's A offsets (at most 8 loads per wave and stage)
+    ring_prologue<SWIGLU, GATHER>(p, lds, cur, a_carry);
     bool after_epilogue = false;
     int sa = 0, sb = 0;  // ring slots of the current tile's first stage
     for (;;) {
@@ -1117,7 +1187,7 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_persistent_kernel(G
             nxt.expert = e;
             nxt.variant = v;
         }
-        ring_run<SWIGLU>(p, lds, cur, nxt, after_epilogue, sa, sb);
+        ring_run<SWIGLU, GATHER>(p, lds, cur, nxt, after_epilogue, sa, sb, a_carry);
         if (!nxt.valid) break;
         cur = nxt;
         q = qn;
@@ -1157,7 +1227,7 @@ constexpr uint32_t decode_lds_bytes() {
     return SWIGLU && MAX_ROWS == 64 ? 3 * (64 + 2 * narrow_cols<SWIGLU, MAX_ROWS>()) * kRowBytes : kRingBytes;
 }
 
-template <bool SWIGLU, int MAX_ROWS>
+template <bool SWIGLU, int MAX_ROWS, bool GATHER>
 __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmParams p) {
     constexpr int COLS = narrow_cols<SWIGLU, MAX_ROWS>();
     constexpr int BNT = SWIGLU ? 2 * COLS : COLS;
@@ -1203,28 +1273,35 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmP
         w.valid = true;
         return w;
     };
+    uint32_t a_carry[8];  // GATHER: the next tile's A offsets, formed where its prologue is issued
+    auto issue = [&](auto ops) {
+        ops.prologue(k_steps);
+        if constexpr (GATHER) {
+#pragma unroll
+            for (int i = 0; i < decltype(ops)::A_LOADS; ++i) a_carry[i] = ops.a_off[i];
+        }
+    };
     auto prologue = [&](const Work& w) {
         if constexpr (MAX_ROWS == 128) {
             if (w.tall) {
-                RingOps<128, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
-                    .prologue(k_steps);
+                issue(RingOps<128, BNT, SWIGLU, kLds, WC, kDecodeStages, GATHER>(p, lds, w.expert, w.col0, w.row0,
+                                                                                 w.row_end));
                 return;
             }
         }
-        RingOps<64, BNT, SWIGLU, kLds, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end)
-            .prologue(k_steps);
+        issue(RingOps<64, BNT, SWIGLU, kLds, WC, kDecodeStages, GATHER>(p, lds, w.expert, w.col0, w.row0, w.row_end));
     };
     auto run = [&](const Work& w, bool wait_all, const auto& hook) {
         using Hook = std::decay_t<decltype(hook)>;
         if constexpr (MAX_ROWS == 128) {
             if (w.tall) {
-                ring_tile<128, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0,
-                                                                                w.row_end, false, wait_all, hook);
+                ring_tile<128, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages, GATHER>(
+                    p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook, 0, 0, false, {}, a_carry);
                 return;
             }
         }
-        ring_tile<64, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages>(p, lds, w.expert, w.col0, w.row0, w.row_end,
-                                                                        false, wait_all, hook);
+        ring_tile<64, BNT, SWIGLU, kLds, Hook, WC, kDecodeStages, GATHER>(
+            p, lds, w.expert, w.col0, w.row0, w.row_end, false, wait_all, hook, 0, 0, false, {}, a_carry);
     };
     int t = blockIdx.x;
     Work cur = locate(t);
@@ -1309,12 +1386,23 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
         const uint32_t lds = rows <= 64 ? decode_lds_bytes<SWIGLU, 64>() : decode_lds_bytes<SWIGLU, 128>();
         int64_t grid = static_cast<int64_t>(device_cu_count()) * (kRingBytes / lds);
         if (tiles < grid) grid = tiles;
-        if (rows <= 64)
-            hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 64>), dim3(static_cast<unsigned>(grid)),
-                               dim3(kRingThreads), 0, stream, q);
-        else
-            hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 128>), dim3(static_cast<unsigned>(grid)),
-                               dim3(kRingThreads), 0, stream, q);
+        auto launch = [&](auto gather_c) {
+            constexpr bool G = decltype(gather_c)::value;
+            if (rows <= 64)
+                hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 64, G>), dim3(static_cast<unsigned>(grid)),
+                                   dim3(kRingThreads), 0, stream, q);
+            else
+                hipLaunchKernelGGL((grouped_gemm_decode_kernel<SWIGLU, 128, G>), dim3(static_cast<unsigned>(grid)),
+                                   dim3(kRingThreads), 0, stream, q);
+        };
+        if constexpr (SWIGLU) {
+            if (p.a_rows != nullptr)
+                launch(std::true_type{});
+            else
+                launch(std::false_type{});
+        } else {
+            launch(std::false_type{});
+        }
         return check_launch("grouped_gemm_decode_kernel");
     }
     if (BM == 256 && BN == 256 && p.k % kStageK == 0) {
@@ -1331,10 +1419,20 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
         if (units < grid) grid = units;
         grid = grid / kNumXcd * kNumXcd;
         if (grid < kNumXcd) grid = kNumXcd;
-        hipLaunchKernelGGL((grouped_gemm_persistent_kernel<SWIGLU>), dim3(static_cast<unsigned>(grid)),
-                           dim3(kRingThreads), 0, stream, p);
+        if constexpr (SWIGLU) {
+            if (p.a_rows != nullptr)
+                hipLaunchKernelGGL((grouped_gemm_persistent_kernel<true, true>), dim3(static_cast<unsigned>(grid)),
+                                   dim3(kRingThreads), 0, stream, p);
+            else
+                hipLaunchKernelGGL((grouped_gemm_persistent_kernel<true, false>), dim3(static_cast<unsigned>(grid)),
+                                   dim3(kRingThreads), 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((grouped_gemm_persistent_kernel<false, false>), dim3(static_cast<unsigned>(grid)),
+                               dim3(kRingThreads), 0, stream, p);
+        }
         return check_launch("grouped_gemm_persistent_kernel");
     }
+    if (p.a_rows != nullptr) return fail(MOE_ERR_UNSUPPORTED, "gathered A rows need K a multiple of 64");
     // The generic kernel maps workgroup b to tile (b % 8) * per_xcd + b / 8 with
     // per_xcd = ceil(tiles / 8), which reaches every tile only when the grid
     // holds all 8 * per_xcd slots: round the upper bound up to a multiple of 8.
@@ -1367,6 +1465,28 @@ int launch_gateup_swiglu(const uint16_t* a, const uint16_t* gate_up, uint16_t* a
     GemmParams p{};
     p.rows = rows;
     p.a = a;
+    p.b = gate_up;
+    p.c = act;
+    p.offsets = offsets;
+    p.k = hidden;
+    p.nb = 2 * intermediate;
+    p.n_out = intermediate;
+    p.ldc = intermediate;
+    p.experts = experts;
+    return launch_gemm_t<256, 256, 2, 2, true>(p, rows, stream);
+}
+
+// launch_gateup_swiglu with A row r read from row a_rows[r] of x (zero when
+// negative): the dispatch's row table instead of its packed copy. Needs the
+// ring kernels (hidden a multiple of 64; the ABI checks it).
+int launch_gateup_swiglu_gathered(const uint16_t* x, const int32_t* a_rows, int64_t x_rows, const uint16_t* gate_up,
+                                  uint16_t* act, const int32_t* offsets, int64_t rows, int64_t hidden,
+                                  int64_t intermediate, int experts, hipStream_t stream) {
+    GemmParams p{};
+    p.rows = rows;
+    p.a = x;
+    p.a_rows = a_rows;
+    p.a_src_rows = x_rows;
     p.b = gate_up;
     p.c = act;
     p.offsets = offsets;

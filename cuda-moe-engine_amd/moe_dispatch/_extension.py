@@ -275,6 +275,27 @@ class HipExtension:
             gate_up.shape[1] // 2, gate_up.shape[0], _stream(x.device))
         self.lib.check(status, "gateup_swiglu_out")
 
+    def gateup_swiglu_gathered_out(self, x, row_src, gate_up, offsets, output):
+        """gateup_swiglu_out with row r of A read from row ``row_src[r]`` of x
+        (zero when negative); output is ``[len(row_src), I]``."""
+        _check(gate_up.dim() == 3 and gate_up.shape[1] % 2 == 0, "expected gate_up[E,2I,H]")
+        _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,
+               "expected contiguous BF16 GPU x[T,H]")
+        _check_gpu_tensor(row_src, x, "row_src")
+        _check(row_src.dtype == torch.int32 and row_src.dim() == 1, "expected int32 row_src[R]")
+        rows = row_src.numel()
+        _check(x.shape[1] % 64 == 0, "gathered gate/up needs hidden a multiple of 64")
+        for name, t in (("gate_up", gate_up), ("offsets", offsets), ("output", output)):
+            _check_gpu_tensor(t, x, name)
+        _check(gate_up.dtype == torch.bfloat16 and gate_up.shape[2] == x.shape[1], "expected BF16 gate_up matching x")
+        _check(offsets.dtype == torch.int32 and offsets.numel() == gate_up.shape[0] + 1, "expected int32 offsets[E+1]")
+        _check(output.shape == (rows, gate_up.shape[1] // 2) and output.dtype == torch.bfloat16,
+               "incorrect grouped-GEMM output buffer")
+        status = self.lib.moe_grouped_gateup_swiglu_gathered(
+            _ptr(x), _ptr(row_src), x.shape[0], _ptr(gate_up), _ptr(output), _ptr(offsets), rows, x.shape[1],
+            gate_up.shape[1] // 2, gate_up.shape[0], _stream(x.device))
+        self.lib.check(status, "gateup_swiglu_gathered_out")
+
     def set_gemm_workgroups(self, workgroups):
         """Bound the persistent grouped GEMM's workgroups (0: one per CU); results do not change."""
         _check(isinstance(workgroups, int) and workgroups >= 0, "workgroups must be a non-negative int")

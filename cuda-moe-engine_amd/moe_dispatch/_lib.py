@@ -13,7 +13,7 @@ from functools import lru_cache
 from pathlib import Path
 
 LIBRARY_NAME = "libmoe_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -47,10 +47,14 @@ _SIGNATURES = {
         _int,
         [_c_void_p, _int] + [_c_void_p] * 8 + [_i64] * 8 + [_int, _c_void_p],
     ),
+    "moe_dispatch_rows": (_int, [_c_void_p] * 7 + [_i64] * 6 + [_c_void_p]),
+    "moe_dispatch_ranked_rows": (_int, [_c_void_p] * 8 + [_i64] * 7 + [_c_void_p]),
     "moe_combine": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 4 + [_c_void_p]),
     "moe_swiglu": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "moe_grouped_gemm": (_int, [_c_void_p] * 4 + [_i64] * 4 + [_c_void_p]),
     "moe_grouped_gateup_swiglu": (_int, [_c_void_p] * 4 + [_i64] * 4 + [_c_void_p]),
+    "moe_grouped_gateup_swiglu_gathered": (_int, [_c_void_p, _c_void_p, _i64] + [_c_void_p] * 3 + [_i64] * 4
+                                           + [_c_void_p]),
     "moe_set_gemm_workgroups": (_int, [_i64]),
 }
 

@@ -247,6 +247,15 @@ class MoEBlock(torch.nn.Module):
             )
         return self._workspaces[key]
 
+    def _experts_gathered(self, state, x):
+        """experts_forward() with the gate/up GEMM reading x through
+        ``transport.row_src`` (after dispatch_rows), not the packed rows."""
+        transport = state.transport
+        ext = self._extension
+        ext.gateup_swiglu_gathered_out(x, transport.row_src, self.gate_up_weight, transport.offsets, state.activated)
+        ext.grouped_gemm_out(state.activated, self.down_weight, transport.offsets, state.expert_output)
+        return state.expert_output
+
     def experts_forward(self, state):
         transport = state.transport
         offsets = transport.offsets
@@ -280,20 +289,43 @@ class MoEBlock(torch.nn.Module):
             if launches is not None and launches.still_valid(self):
                 return launches(self, x)
         state = self.workspace(x)
+        fused = self.implementation == "cuda_fused"
         # The fused router does the dispatch's counting pass when the shape allows.
-        ranked = self.implementation == "cuda_fused" and state.transport.rank_tile > 0
+        ranked = fused and state.transport.rank_tile > 0
+        gathered = fused and _gathers(x, self.config.topk)
         ids32, ids64, weights = self._route(x, state.transport if ranked else None)
-        if ranked:
-            state.transport.dispatch_ranked(x, ids32)
+        transport = state.transport
+        if gathered:
+            # No packed copy: the gate/up GEMM reads x through the row table.
+            if ranked:
+                transport.dispatch_ranked_rows(ids32)
+            else:
+                transport.dispatch_rows(ids32)
+            output = self._experts_gathered(state, x)
         else:
-            state.transport.dispatch(x, ids32, ids64)
-        output = self.experts_forward(state)
-        state.transport.combine(output, weights)
+            if ranked:
+                transport.dispatch_ranked(x, ids32)
+            else:
+                transport.dispatch(x, ids32, ids64)
+            output = self.experts_forward(state)
+        transport.combine(output, weights)
         if self.implementation == "cuda_fused":
             # Every operator above validated its tensors; later calls of this
             # shape reuse the checked arguments.
             self._launches[(x.shape[0], x.device)] = _FusedLaunches(self, x, state)
         return state.transport.output
+
+
+def _gathers(x, topk):
+    """Whether the fused forward skips the packed copy, the gate/up GEMM reading
+    x through the dispatch's row table. It needs the ring kernels (hidden a
+    multiple of 64) and x below 2 GiB, and pays off from top-3 on: the gathered
+    GEMM waits longer on its A loads than on the just-written packed rows
+    (MFMA busy 0.67 against 0.70 at H=4096, I=14336, E=8, top-2: gate/up +2%,
+    forward +0.9%; H=1024, I=2048, E=16: gate/up +5%), while with K rows per
+    token the copy it saves grows with K (H=2048, I=1408, E=64, top-6: dispatch
+    39 -> 7 us, gate/up unchanged, forward -3.8%)."""
+    return topk >= 3 and x.shape[1] % 64 == 0 and x.numel() * x.element_size() < 2**31
 
 
 class _FusedLaunches:
@@ -328,21 +360,36 @@ class _FusedLaunches:
         self.router = (block.routing_bias.data_ptr(), ids32.data_ptr(), ids64.data_ptr(), weights.data_ptr(),
                        None, scratch.data_ptr(), scratch.numel() * scratch.element_size(),
                        tokens, hidden, cfg.experts, cfg.topk)
-        # A ranked route (the router counts for the dispatch) whenever the shape has one, as in forward().
+        # A ranked route (the router counts for the dispatch) whenever the shape
+        # has one, and the row table instead of the packed copy whenever the
+        # gate/up GEMM can gather, as in forward().
         self.ranked = t.rank_tile > 0
+        self.gathered = _gathers(x, cfg.topk)
+        index = (ids32.data_ptr(), t.counts.data_ptr(), t.offsets.data_ptr(), t.slots.data_ptr())
         if self.ranked:
             self.router += (t.tile_ranks.data_ptr(), t.tile_counts.data_ptr(), t.tile_counts.numel() * 4)
-            self.dispatch = (_lib.DTYPE_BF16, ids32.data_ptr(), t.counts.data_ptr(), t.offsets.data_ptr(),
-                             t.slots.data_ptr(), t.packed.data_ptr(), t.inverse.data_ptr(), t.tile_ranks.data_ptr(),
-                             t.tile_counts.data_ptr(), t.tile_counts.numel() * 4, t.rank_tile, tokens, hidden,
-                             cfg.experts, cfg.topk, t.alignment, rows, int(bool(t.vectorized)))
+            ranked_table = (t.tile_ranks.data_ptr(), t.tile_counts.data_ptr(), t.tile_counts.numel() * 4, t.rank_tile)
+        if self.gathered:
+            after = (t.inverse.data_ptr(), t.row_src.data_ptr())
+            if self.ranked:
+                self.dispatch = index + after + ranked_table + (tokens, cfg.experts, cfg.topk, t.alignment, rows)
+            else:
+                self.dispatch = index + after + (t.scratch.data_ptr(), t.scratch.numel() * t.scratch.element_size(),
+                                                 tokens, cfg.experts, cfg.topk, t.alignment, rows)
+            # moe_grouped_gateup_swiglu_gathered after x.
+            self.gateup = (t.row_src.data_ptr(), tokens, block.gate_up_weight.data_ptr(), state.activated.data_ptr(),
+                           t.offsets.data_ptr(), rows, hidden, cfg.intermediate, cfg.experts)
         else:
-            self.dispatch = (_lib.DTYPE_BF16, ids32.data_ptr(), t.counts.data_ptr(), t.offsets.data_ptr(),
-                             t.slots.data_ptr(), t.packed.data_ptr(), t.inverse.data_ptr(), t.scratch.data_ptr(),
-                             t.scratch.numel() * t.scratch.element_size(), tokens, hidden, cfg.experts, cfg.topk,
-                             t.alignment, rows, int(bool(t.vectorized)))
-        self.gateup = (t.packed.data_ptr(), block.gate_up_weight.data_ptr(), state.activated.data_ptr(),
-                       t.offsets.data_ptr(), rows, hidden, cfg.intermediate, cfg.experts)
+            packed = (t.packed.data_ptr(), t.inverse.data_ptr())
+            if self.ranked:
+                self.dispatch = (_lib.DTYPE_BF16,) + index + packed + ranked_table + (
+                    tokens, hidden, cfg.experts, cfg.topk, t.alignment, rows, int(bool(t.vectorized)))
+            else:
+                self.dispatch = (_lib.DTYPE_BF16,) + index + packed + (
+                    t.scratch.data_ptr(), t.scratch.numel() * t.scratch.element_size(), tokens, hidden, cfg.experts,
+                    cfg.topk, t.alignment, rows, int(bool(t.vectorized)))
+            self.gateup = (t.packed.data_ptr(), block.gate_up_weight.data_ptr(), state.activated.data_ptr(),
+                           t.offsets.data_ptr(), rows, hidden, cfg.intermediate, cfg.experts)
         self.down = (state.activated.data_ptr(), block.down_weight.data_ptr(), state.expert_output.data_ptr(),
                      t.offsets.data_ptr(), rows, hidden, cfg.intermediate, cfg.experts)
         self.combine = (state.expert_output.data_ptr(), _lib.DTYPE_BF16, t.inverse.data_ptr(), weights.data_ptr(),
@@ -370,16 +417,44 @@ class _FusedLaunches:
         router_weight, split_of = block._router_split_plan()
         if self.ranked:
             lib.check(lib.moe_router_fused_ranked(x_ptr, router_weight, *self.router, stream), "router_fused_out")
-            block._router_split_of = split_of
-            lib.check(lib.moe_dispatch_ranked(x_ptr, *self.dispatch, stream), "dispatch")
         else:
             lib.check(lib.moe_router_fused(x_ptr, router_weight, *self.router, stream), "router_fused_out")
-            block._router_split_of = split_of
-            lib.check(lib.moe_dispatch(x_ptr, *self.dispatch, stream), "dispatch")
-        lib.check(lib.moe_grouped_gateup_swiglu(*self.gateup, stream), "gateup_swiglu_out")
+        block._router_split_of = split_of
+        if self.gathered:
+            if self.ranked:
+                lib.check(lib.moe_dispatch_ranked_rows(*self.dispatch, stream), "dispatch")
+            else:
+                lib.check(lib.moe_dispatch_rows(*self.dispatch, stream), "dispatch")
+            lib.check(lib.moe_grouped_gateup_swiglu_gathered(x_ptr, *self.gateup, stream), "gateup_swiglu_out")
+        else:
+            if self.ranked:
+                lib.check(lib.moe_dispatch_ranked(x_ptr, *self.dispatch, stream), "dispatch")
+            else:
+                lib.check(lib.moe_dispatch(x_ptr, *self.dispatch, stream), "dispatch")
+            lib.check(lib.moe_grouped_gateup_swiglu(*self.gateup, stream), "gateup_swiglu_out")
         lib.check(lib.moe_grouped_gemm(*self.down, stream), "grouped_gemm_out")
         lib.check(lib.moe_combine(*self.combine, stream), "combine_out")
         return self.output
+
+    def stage_calls(self, x):
+        """Each stage of __call__ as a zero-argument callable on the current
+        stream (the router with the split it holds), for per-stage timing."""
+        lib, x_ptr = self.lib, x.data_ptr()
+
+        def bind(name, *args):
+            def run():
+                lib.check(getattr(lib, name)(*args, current_stream_handle(self.device_index)), name)
+            return run
+
+        router = "moe_router_fused_ranked" if self.ranked else "moe_router_fused"
+        if self.gathered:
+            dispatch = bind("moe_dispatch_ranked_rows" if self.ranked else "moe_dispatch_rows", *self.dispatch)
+            gateup = bind("moe_grouped_gateup_swiglu_gathered", x_ptr, *self.gateup)
+        else:
+            dispatch = bind("moe_dispatch_ranked" if self.ranked else "moe_dispatch", x_ptr, *self.dispatch)
+            gateup = bind("moe_grouped_gateup_swiglu", *self.gateup)
+        return {"router": bind(router, x_ptr, None, *self.router), "dispatch": dispatch, "gateup_swiglu": gateup,
+                "down": bind("moe_grouped_gemm", *self.down), "combine": bind("moe_combine", *self.combine)}
 
 
 @torch.inference_mode()

@@ -18,7 +18,10 @@ the reference's do); ``ops.dispatch`` checks them.
 A workspace also holds the buffers of a ranked route (``tile_ranks``,
 ``tile_counts``; ``rank_tile`` tokens per tile, 0 when the shape has none):
 the fused router can write the in-tile ranks and per-tile counts itself,
-after which ``dispatch_ranked`` runs only the pack pass.
+after which ``dispatch_ranked`` runs only the pack pass. ``dispatch_rows`` and
+``dispatch_ranked_rows`` write the same layout without copying rows: instead
+of ``packed``, ``row_src`` receives each packed row's token (-1 for padding),
+which the gathered gate/up GEMM reads x through.
 
 One workspace serves one invocation at a time: its outputs are views that the
 next call overwrites.
@@ -80,6 +83,13 @@ class _Bound:
                                  ws.packed.data_ptr(), ws.inverse.data_ptr(), ws.tile_ranks.data_ptr(),
                                  ws.tile_counts.data_ptr(), ws.tile_counts.numel() * 4, ws.rank_tile, tokens,
                                  hidden, experts, topk, ws.alignment, ws.capacity_rows, int(bool(ws.vectorized)))
+        index = (ws.counts.data_ptr(), ws.offsets.data_ptr(), ws.slots.data_ptr(), ws.inverse.data_ptr(),
+                 ws.row_src.data_ptr())
+        self.rows_after_ids = index + (ws.scratch.data_ptr(), nbytes, tokens, experts, topk, ws.alignment,
+                                       ws.capacity_rows)
+        self.ranked_rows_after_ids = index + (ws.tile_ranks.data_ptr(), ws.tile_counts.data_ptr(),
+                                              ws.tile_counts.numel() * 4, ws.rank_tile, tokens, experts, topk,
+                                              ws.alignment, ws.capacity_rows)
         self.output = ws.output.data_ptr()
         self.inverse = ws.inverse.data_ptr()
         self.x_shape = (tokens, hidden)
@@ -112,6 +122,16 @@ class _Bound:
         status = self.lib.moe_dispatch_ranked(x.data_ptr(), self.code, ids32.data_ptr(), *self.ranked_after_ids,
                                               current_stream_handle(self.device_index))
         self.lib.check(status, self.name)
+
+    def dispatch_rows(self, ids32, ranked):
+        self._require(ids32, self.ids_shape, torch.int32, "ids")
+        if ranked:
+            status = self.lib.moe_dispatch_ranked_rows(ids32.data_ptr(), *self.ranked_rows_after_ids,
+                                                       current_stream_handle(self.device_index))
+        else:
+            status = self.lib.moe_dispatch_rows(ids32.data_ptr(), *self.rows_after_ids,
+                                                current_stream_handle(self.device_index))
+        self.lib.check(status, "dispatch_rows")
 
     def combine(self, expert_output, weights):
         # Any row count that holds every assignment (the reference's combine_out
@@ -162,6 +182,7 @@ class CudaWorkspace:
             "scratch": ((max(self.extension.scratch_bytes(tokens, experts, topk), 4),), torch.uint8),
             "tile_ranks": ((assignments if tiles else 1,), torch.int32),
             "tile_counts": ((max(tiles * experts, 1),), torch.int32),
+            "row_src": ((rows,), torch.int32),
         }
         self._names = tuple(layout)
         for name, (shape, kind) in layout.items():
@@ -178,6 +199,17 @@ class CudaWorkspace:
         if self.rank_tile <= 0:
             raise RuntimeError("this workspace's shape has no ranked route (rank_tile == 0)")
         self._bound.dispatch_ranked(x, ids32)
+
+    def dispatch_rows(self, ids32):
+        """The dispatch layout (counts, offsets, slots, inverse) without copying
+        rows: ``row_src`` receives each packed row's token, -1 for padding rows."""
+        self._bound.dispatch_rows(ids32, ranked=False)
+
+    def dispatch_ranked_rows(self, ids32):
+        """dispatch_rows() after a ranked route (as ``dispatch_ranked``)."""
+        if self.rank_tile <= 0:
+            raise RuntimeError("this workspace's shape has no ranked route (rank_tile == 0)")
+        self._bound.dispatch_rows(ids32, ranked=True)
 
     def combine(self, expert_output, weights):
         """Hot path: expert_output[R, H] (R >= T*K) of the workspace dtype, fp32 weights[T,K]."""

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 6
+#define MOE_ABI_VERSION 7
 
 typedef enum {
     MOE_DTYPE_F32 = 0,
@@ -193,6 +193,27 @@ int moe_dispatch_ranked(const void* x, int dtype, const int32_t* ids, int32_t* c
                         int vectorized, void* stream);
 
 /*
+ * The dispatch layout without the rows, for moe_grouped_gateup_swiglu_gathered:
+ * counts, offsets, slots and inverse exactly as moe_dispatch writes them, and
+ * instead of packed rows the row table row_src (packed_rows int32):
+ *   row_src[inverse[p]] = p / K for every assignment p, row_src[r] = -1 for the
+ *   padding rows [offsets[e] + counts[e], offsets[e+1]); rows >= offsets[E]
+ *   are not written.
+ * moe_dispatch_rows counts with its scratch like moe_dispatch;
+ * moe_dispatch_ranked_rows takes a ranked route's ranks and tile counts like
+ * moe_dispatch_ranked. No counterpart in the reference (its dispatch always
+ * copies the rows): the expert GEMM reads x through the table instead, which
+ * saves writing and reading back T*K rows.
+ */
+int moe_dispatch_rows(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* slots, int32_t* inverse,
+                      int32_t* row_src, void* scratch, int64_t scratch_bytes, int64_t tokens, int64_t experts,
+                      int64_t topk, int64_t alignment, int64_t packed_rows, void* stream);
+int moe_dispatch_ranked_rows(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* slots,
+                             int32_t* inverse, int32_t* row_src, const int32_t* ranks, const int32_t* tile_counts,
+                             int64_t tile_counts_bytes, int64_t tile_tokens, int64_t tokens, int64_t experts,
+                             int64_t topk, int64_t alignment, int64_t packed_rows, void* stream);
+
+/*
  * Weighted combine: out[t] = round(sum_k w[t,k] * float(y[inverse[t,k]])),
  * fp32 products and running sum in k order (no fused multiply-add), rows
  * outside [0, packed_rows) skipped, no atomics.
@@ -234,6 +255,18 @@ int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offse
 int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
                               const int32_t* offsets, int64_t rows, int64_t hidden,
                               int64_t intermediate, int64_t experts, void* stream);
+
+/*
+ * moe_grouped_gateup_swiglu with row r of A read from row row_src[r] of x
+ * ([x_rows, hidden] bf16; a negative entry reads zeros): with the row table
+ * of moe_dispatch_rows this equals moe_grouped_gateup_swiglu on that
+ * dispatch's packed rows, bit for bit. No counterpart in the reference (its
+ * grouped GEMM reads the packed copy). Requires hidden % 64 == 0 and x below
+ * 2 GiB.
+ */
+int moe_grouped_gateup_swiglu_gathered(const void* x, const int32_t* row_src, int64_t x_rows, const void* gate_up,
+                                       void* act, const int32_t* offsets, int64_t rows, int64_t hidden,
+                                       int64_t intermediate, int64_t experts, void* stream);
 
 /*
  * Upper bound on the workgroups of the persistent grouped GEMM (both

@@ -148,3 +148,32 @@ def test_error_surfaces_as_runtime_error():
     lib = _lib.load_library()
     with pytest.raises(_lib.MoeHipError, match="1..64"):
         lib.check(lib.moe_topk_route(None, None, None, None, None, 5, 65, 2, None), "topk")
+
+
+def test_row_table_entry_points_check_their_arguments_without_launching():
+    """moe_dispatch_rows, moe_dispatch_ranked_rows and the gathered gate/up GEMM
+    refuse bad shapes, sizes and pointers before any launch (stand-in addresses,
+    never dereferenced)."""
+    lib = _lib.load_library()
+    A = 1 << 20
+    scratch = lib.moe_dispatch_scratch_bytes(10, 8, 2)
+    # ids, counts, offsets, slots, inverse, row_src, scratch, bytes, T, E, K, a, rows
+    assert lib.moe_dispatch_rows(A, A, A, A, A, A, A, scratch, 10, 8, 2, 8, 79, None) == 4  # rows < capacity (80)
+    assert b"row table" in lib.moe_last_error()
+    assert lib.moe_dispatch_rows(A, A, A, A, A, A, A, scratch, 10, 65, 2, 1, 20, None) == 2  # experts
+    assert lib.moe_dispatch_rows(A, A, A, A, A, None, A, scratch, 10, 8, 2, 1, 20, None) == 1  # null table
+    assert lib.moe_dispatch_rows(A, A, A, A, A, A + 2, A, scratch, 10, 8, 2, 1, 20, None) == 1  # misaligned
+    assert lib.moe_dispatch_rows(A, A, A, A, A, A, A, scratch - 4, 10, 8, 2, 1, 20, None) == 4  # scratch
+    # ranked: the tile must be the route's, then the table size
+    r = (A, A, A, A, A, A, A, A)
+    assert lib.moe_dispatch_ranked_rows(*r, 224, 32, 100, 8, 2, 1, 200, None) == 1
+    assert b"not the ranked route's tile" in lib.moe_last_error()
+    assert lib.moe_dispatch_ranked_rows(*r, 223, 16, 100, 8, 2, 1, 200, None) == 4
+    # gathered gate/up: x, row_src, x_rows, gate_up, act, offsets, rows, H, I, E
+    assert lib.moe_grouped_gateup_swiglu_gathered(A, A, 16, A, A, A, 16, 96, 64, 1, None) == 2
+    assert b"multiple of 64" in lib.moe_last_error()
+    assert lib.moe_grouped_gateup_swiglu_gathered(A, A, 1 << 18, A, A, A, 16, 4096, 64, 1, None) == 3  # 2 GiB
+    assert lib.moe_grouped_gateup_swiglu_gathered(A + 8, A, 16, A, A, A, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gateup_swiglu_gathered(A, A + 2, 16, A, A, A, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gateup_swiglu_gathered(A, None, 16, A, A, A, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gateup_swiglu_gathered(A, A, 16, A, A, A, 0, 64, 64, 1, None) == 0  # no rows

@@ -5,7 +5,10 @@ Stage by stage, each stage fed the kernels' own inputs:
     (K+1)-th margin is not a near-tie (the fused router sums its dot products
     in its own order; selection on the kernel's logits is bit-exact in
     test_gpu_router.py); the downstream oracle uses the kernel's routing;
-  * dispatch: counts, offsets, inverse and packed rows bit-exact;
+  * dispatch: counts, offsets, inverse and packed rows bit-exact (when the
+    gate/up GEMM gathers its rows from x, which the block does from top-3 on
+    with hidden a multiple of 64, the row table instead: each used row's
+    token, -1 for padding; the GEMM oracle then reads x through it);
   * gate/up + SwiGLU and down GEMM: at least 99.99% of elements identical to
     the MFMA-order oracle, the rest within 2 bf16 steps;
   * combine: bit-exact.
@@ -50,6 +53,24 @@ def _run_block(cfg, tokens, pattern, seed, bias=None):
     return block, x, out, ids32, weights, state
 
 
+def _gate_up_rows(block, x, transport, layout, topk):
+    """The rows the gate/up GEMM read: the packed copy, or for a gathered forward
+    (no copy) x through the row table, which must map every used row to its
+    token and every padding row to -1."""
+    used = int(layout["offsets"][-1])
+    if not block._launches[(x.shape[0], x.device)].gathered:
+        return transport.packed
+    src = transport.row_src[:used]
+    expected = np.full(used, -1, np.int64)
+    inverse = layout["inverse"].reshape(-1)
+    expected[inverse] = np.arange(inverse.size) // topk
+    np.testing.assert_array_equal(to_np(src), expected)
+    rows = torch.zeros_like(transport.packed)
+    ok = src >= 0
+    rows[:used][ok] = x.index_select(0, src[ok].long())
+    return rows
+
+
 def _check_block(cfg, tokens, pattern="balanced", seed=0, bias=None, large_i=False):
     block, x, out, ids32, weights, state = _run_block(cfg, tokens, pattern, seed, bias)
     xf = to_np(x)
@@ -75,7 +96,7 @@ def _check_block(cfg, tokens, pattern="balanced", seed=0, bias=None, large_i=Fal
     used = int(layout["offsets"][-1])
     rows = transport.capacity_rows
     packed_ref, _ = oracle.pack(xf, layout, cfg.topk, rows)
-    packed = to_np(transport.packed)
+    packed = to_np(_gate_up_rows(block, x, transport, layout, cfg.topk))
     np.testing.assert_array_equal(packed[:used], packed_ref[:used])
     offsets = layout["offsets"]
     # Expert GEMMs, each on the kernels' own input.
@@ -296,11 +317,11 @@ def _sample_rows(offsets, counts, per_expert, rng):
     return np.asarray(rows, dtype=np.int64), np.asarray(sample_offsets, dtype=np.int64)
 
 
-def _check_expert_span(state, block, offsets, counts, expert):
+def _check_expert_span(state, block, packed_rows, offsets, counts, expert):
     """Both GEMMs over one whole expert span (every row, every column) against the
     MFMA-order oracle (the C checker), each on the kernels' own input."""
     lo, n = int(offsets[expert]), int(counts[expert])
-    packed = to_np(state.transport.packed[lo:lo + n])
+    packed = to_np(packed_rows[lo:lo + n])
     act = to_np(state.activated[lo:lo + n])
     eo = to_np(state.expert_output[lo:lo + n])
     span = np.array([0, n])
@@ -337,18 +358,19 @@ def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, to
     np.testing.assert_array_equal(to_np(transport.offsets), layout["offsets"])
     np.testing.assert_array_equal(to_np(transport.inverse), layout["inverse"])
     np.testing.assert_array_equal(to_np(transport.slots).reshape(-1), layout["slots"])
+    packed_rows = _gate_up_rows(block, x, transport, layout, cfg.topk)
     inv = transport.inverse.reshape(-1).long()
-    gathered = transport.packed.index_select(0, inv).view(tokens, cfg.topk, cfg.hidden)
+    gathered = packed_rows.index_select(0, inv).view(tokens, cfg.topk, cfg.hidden)
     assert torch.equal(gathered, x[:, None, :].expand_as(gathered))
     offsets, counts = layout["offsets"], layout["counts"]
     for e in range(cfg.experts):
-        pad = transport.packed[int(offsets[e]) + int(counts[e]):int(offsets[e + 1])]
+        pad = packed_rows[int(offsets[e]) + int(counts[e]):int(offsets[e + 1])]
         assert int(torch.count_nonzero(pad)) == 0
     # Expert GEMMs on sampled rows of every expert, each on the kernels' own input.
     rows, sample_offsets = _sample_rows(offsets, counts, per_expert, rng)
     rows_t = torch.from_numpy(rows).cuda()
     gate_up, down = LazyExpertWeights(block.gate_up_weight), LazyExpertWeights(block.down_weight)
-    packed_s = to_np(transport.packed.index_select(0, rows_t))
+    packed_s = to_np(packed_rows.index_select(0, rows_t))
     act_s = to_np(state.activated.index_select(0, rows_t))
     proj_ref = oracle.bf16_round(oracle.grouped_gemm(packed_s, gate_up, sample_offsets))
     assert_near_bit_exact(act_s, oracle.swiglu(proj_ref, len(rows)), max_fraction=2e-4, max_steps=2.0)
@@ -376,7 +398,7 @@ def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, to
     assert rel_l2(got, dense) <= (REL_L2_LARGE_I if large_i else REL_L2)
     if full_span:
         nonempty = [e for e in range(cfg.experts) if counts[e] > 0]
-        _check_expert_span(state, block, offsets, counts, min(nonempty, key=lambda e: counts[e]))
+        _check_expert_span(state, block, packed_rows, offsets, counts, min(nonempty, key=lambda e: counts[e]))
     return counts
 
 
