@@ -277,7 +277,8 @@ def measured_traffic(config, kernels):
     return total
 
 
-def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, launch_us, cus=None):
+def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, launch_us, cus=None,
+                    gathered=False):
     """Roofline entry for the gate/up GEMM + SwiGLU launch.
 
     Algorithmic bytes per launch: the weights of the experts that hold rows
@@ -289,7 +290,9 @@ def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, 
     ``csrc/gemm.hip``): the weight-streaming (decode) kernel when the buffer
     has at most 128 rows, or at most 128 per expert while the 256 x 256 tiles
     (rows spread evenly over the experts) would number fewer than the CUs
-    (``cus``; default: the current GPU's, 256 without one).
+    (``cus``; default: the current GPU's, 256 without one). ``gathered``: the
+    forward's gate/up GEMM read its rows from x through the row table (the
+    kernels' GATHER instances).
     """
     import torch
 
@@ -303,7 +306,11 @@ def gateup_roofline(config, counts, packed_rows, hidden, inter, n_assign, flop, 
         cus = torch.cuda.get_device_properties(0).multi_processor_count if torch.cuda.is_available() else 256
     wide_tiles = experts * ceil_div(ceil_div(packed_rows, experts), 256) * ceil_div(inter, 128)
     decode = hidden % 64 == 0 and (packed_rows <= 128 or (packed_rows <= 128 * experts and wide_tiles < cus))
-    kernel = "grouped_gemm_decode_kernel<true>" if decode else "grouped_gemm_persistent_kernel<true>"
+    g = "true" if gathered else "false"
+    if decode:
+        kernel = f"grouped_gemm_decode_kernel<true, {64 if packed_rows <= 64 else 128}, {g}>"
+    else:
+        kernel = f"grouped_gemm_persistent_kernel<true, {g}>"
     entry = {"kernel": kernel + " (gate/up GEMM + SwiGLU epilogue)"}
     if flop / byte < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
         achieved = byte / (launch_us * 1e-6) / 1e9
@@ -367,7 +374,7 @@ def transport_bench(args):
     comb_bytes = combine_bytes(tokens, hidden, topk)
     d_gbs = disp_bytes / (d_us * 1e-6) / 1e9
     c_gbs = comb_bytes / (c_us * 1e-6) / 1e9
-    traffic = measured_traffic(args.config, ("count_rank_kernel", "pack_kernel<16, false>"))
+    traffic = measured_traffic(args.config, ("count_rank_kernel", "pack_kernel<16, false, false>"))
     result = {
         "metric": "MoE block fwd latency (us) + expert TFLOP/s % bf16 MFMA peak; dispatch GB/s",
         "value": round(mean_us, 2),
@@ -561,7 +568,8 @@ def main(argv=None):
         "combine_gbs": round(comb_bytes / (stages["combine"]["mean_us"] * 1e-6) / 1e9, 1),
         "expert_counts": counts.tolist(),
         "roofline": gateup_roofline(args.config, counts, block.workspace(x).transport.packed.shape[0],
-                                    hidden, inter, n_assign, gateup_flop, t_gu),
+                                    hidden, inter, n_assign, gateup_flop, t_gu,
+                                    gathered=block._launches[(x.shape[0], x.device)].gathered),
     }
     if not args.no_torch_variant:
         try:

@@ -38,8 +38,8 @@ def test_measured_traffic_sums_kernels(tmp_path, monkeypatch):
 
 def test_committed_traffic_table_covers_the_bench_kernels():
     table = json.loads((ROOT / "profiles" / "hbm_traffic.json").read_text())
-    assert "grouped_gemm_persistent_kernel<true>" in table["c4_t4096"]
-    assert {"count_rank_kernel", "pack_kernel<16, false>"} <= set(table["c2_transport"])
+    assert "grouped_gemm_persistent_kernel<true, false>" in table["c4_t4096"]
+    assert {"count_rank_kernel", "pack_kernel<16, false, false>"} <= set(table["c2_transport"])
 
 
 def test_gateup_roofline_picks_the_bound_by_intensity():
@@ -50,20 +50,22 @@ def test_gateup_roofline_picks_the_bound_by_intensity():
     dec = bench.gateup_roofline("none", np.array([1, 0, 0, 0, 0, 1, 0, 0]), 58, h, i, 2, 4.0 * 2 * h * i, 100.0)
     weights = 2 * 2 * (2 * i * h)
     assert dec["bound"] == "hbm" and dec["unit"] == "GB/s" and dec["peak"] == bench.HBM_PEAK_GBS
-    assert dec["kernel"].startswith("grouped_gemm_decode_kernel<true>")
+    assert dec["kernel"].startswith("grouped_gemm_decode_kernel<true, 64, false>")
     assert weights < dec["bytes_per_launch"] < weights * 1.001
     assert abs(dec["achieved"] - dec["bytes_per_launch"] / 100e-6 / 1e9) < 0.1
     # Prefill: 8192 assignments over 8 experts is far past the ridge point.
     pre = bench.gateup_roofline("none", np.array([1024] * 8), 8248, h, i, 8192, 4.0 * 8192 * h * i, 1000.0)
     assert pre["bound"] == "mfma" and pre["unit"] == "TFLOP/s"
-    assert pre["kernel"].startswith("grouped_gemm_persistent_kernel<true>")
+    assert pre["kernel"].startswith("grouped_gemm_persistent_kernel<true, false>")
+    gathered = bench.gateup_roofline("none", np.array([1024] * 8), 8248, h, i, 8192, 1.0, 1.0, gathered=True)
+    assert gathered["kernel"].startswith("grouped_gemm_persistent_kernel<true, true>")
     assert abs(pre["achieved"] - 4.0 * 8192 * h * i / 1e-3 / 1e12) < 0.1
     assert list(pre)[0] == "bound"
     # 320 rows over 8 experts (T=128, H=512, I=1024): 64 wide tiles for 256 CUs, so
     # the launcher takes the weight-streaming kernel; with 32 CUs the wide one.
     c1 = (np.array([32] * 8), 320, 512, 1024, 256, 4.0 * 256 * 512 * 1024, 10.0)
-    assert bench.gateup_roofline("none", *c1, cus=256)["kernel"].startswith("grouped_gemm_decode_kernel<true>")
-    assert bench.gateup_roofline("none", *c1, cus=32)["kernel"].startswith("grouped_gemm_persistent_kernel<true>")
+    assert bench.gateup_roofline("none", *c1, cus=256)["kernel"].startswith("grouped_gemm_decode_kernel<true, 128, ")
+    assert bench.gateup_roofline("none", *c1, cus=32)["kernel"].startswith("grouped_gemm_persistent_kernel<true, ")
 
 
 def test_byte_models_and_workload_bias_equal_the_oracle():
