@@ -160,3 +160,29 @@ def test_gathered_gateup_rejects_hidden_not_a_multiple_of_64(ext):
     out = torch.empty(8, 8, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(Exception, match="multiple of 64"):
         ext.gateup_swiglu_gathered_out(x, table, gate_up, offsets, out)
+
+
+@pytest.mark.parametrize("cfg,tokens,gathers", [
+    ((2048, 1408, 64, 6), 700, True),   # top-6: the row table
+    ((256, 128, 16, 3), 300, True),     # top-3, hidden a multiple of 64
+    ((512, 1024, 8, 2), 128, False),    # top-2 packs (the gathered GEMM's loads cost more than the copy)
+    ((96, 256, 8, 4), 100, False),      # hidden not a multiple of 64: the generic GEMM cannot gather
+])
+def test_block_forward_gathers_from_top3_on_and_matches_the_packed_forward(monkeypatch, cfg, tokens, gathers):
+    """The block's forward, gathered or packed, is the same bit for bit."""
+    from moe_dispatch import layer
+    from moe_dispatch.layer import MoEBlock, MoEConfig
+
+    config = MoEConfig(*cfg)
+    block = MoEBlock(config, device="cuda", implementation="cuda_fused", seed=3)
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(tokens, config.hidden, device="cuda", generator=gen).bfloat16()
+    first = block(x).clone()
+    assert block._launches[(tokens, x.device)].gathered == gathers
+    again = block(x).clone()  # the pre-bound launches
+    monkeypatch.setattr(layer, "_gathers", lambda x, topk: False)
+    packed_block = MoEBlock(config, device="cuda", implementation="cuda_fused", seed=3)
+    packed = packed_block(x).clone()
+    assert not packed_block._launches[(tokens, x.device)].gathered
+    torch.cuda.synchronize()
+    assert torch.equal(first, packed) and torch.equal(again, packed)

@@ -19,6 +19,7 @@ pytestmark = gpu
     (MoEConfig(512, 1024, 8, 2), 128),      # C1 shape
     (MoEConfig(1024, 2048, 16, 2), 256),    # C3 shape
     (MoEConfig(4096, 14336, 8, 2), 16),     # C4 decode shape
+    (MoEConfig(2048, 1408, 64, 6), 600),    # C5 shape (top-6: the row table and the gathered gate/up GEMM)
 ])
 def test_graph_replays_match_eager(cfg, tokens):
     block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=0)
