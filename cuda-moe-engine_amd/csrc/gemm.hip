@@ -428,33 +428,34 @@ struct RingOps {
                                        int64_t row0, int64_t row_end)
         : RingOps(p, lds_, tile_rsrc(p, expert, col0, row0, row_end)) {}
 
-    // From a tile's resources already formed (a chained next tile's).
-    __device__ __forceinline__ RingOps(const GemmParams& p, char* lds_, const Rsrc& r) : lds(lds_) {
+    // From a tile's resources already formed: a chained next tile's, or a
+    // gathered tile's whose A offsets were carried in.
+    __device__ __forceinline__ RingOps(const GemmParams& p, char* lds_, const Rsrc& res) : lds(lds_) {
         const int lane = threadIdx.x & 63;
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int64_t K = p.k;
-        rsrc_a = r.a;
-        rsrc_b = r.b;
+        rsrc_a = res.a;
+        rsrc_b = res.b;
         const int lrow = lane >> 3;
         const int pchunk = lane & 7;
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) a_off[i] = r.a_off[i];
+        for (int i = 0; i < A_LOADS; ++i) a_off[i] = res.a_off[i];
 #pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-        const int r = (wave * B_LOADS + i) * 8 + lrow;
-        int64_t brow;
-        if constexpr (SWIGLU) {
-            // Wave column wc owns gate columns [wc*WTN/2, (wc+1)*WTN/2) of the
-            // tile and the matching up rows (I further on).
-            const int wcol = r / WTN, w = r % WTN;
-            static constexpr int HALF = WTN / 2;
-            const int64_t col = wcol * HALF + (w % HALF);  // from the tile's first column
-            brow = (w < HALF) ? col : p.n_out + col;
-        } else {
-            brow = r;
+        for (int i = 0; i < B_LOADS; ++i) {
+            const int r = (wave * B_LOADS + i) * 8 + lrow;
+            int64_t brow;
+            if constexpr (SWIGLU) {
+                // Wave column wc owns gate columns [wc*WTN/2, (wc+1)*WTN/2) of the
+                // tile and the matching up rows (I further on).
+                const int wcol = r / WTN, w = r % WTN;
+                static constexpr int HALF = WTN / 2;
+                const int64_t col = wcol * HALF + (w % HALF);  // from the tile's first column
+                brow = (w < HALF) ? col : p.n_out + col;
+            } else {
+                brow = r;
+            }
+            b_off[i] = static_cast<uint32_t>((brow * K + (pchunk ^ ring_key(r)) * 8) * 2);
         }
-        b_off[i] = static_cast<uint32_t>((brow * K + (pchunk ^ ring_key(r)) * 8) * 2);
-    }
     }
     // Load l of stage kt into ring slot st, of A and of B (of this tile, or of
     // the tile whose resources are given).

@@ -682,10 +682,12 @@ __global__ __launch_bounds__(kDirectWaves * 64) void router_direct_kernel(
 // four waves split the weight fragments (wave w: fragments w*FW .. w*FW+FW-1
 // of F = ceil(6E/16)), each over the whole k range, so no wave partials need
 // adding; every wave loads the four token fragments itself (they come from
-// L1/L2 after the first). Loads run up to about 40 ahead of the multiplies:
-// the LDS ring kernel this replaces (E = 64, H = 2048) held three 28 KiB
-// stages in flight per CU, and at about 2.5 us of load latency that bounded it
-// near 34 GB/s per CU (25-37 us at 8192 tokens).
+// L1/L2 after the first). Loads run up to about 40 ahead of the multiplies.
+// At E = 64, H = 2048, 8192 tokens: 23-24 us, against 25-37 us for the LDS
+// ring kernel. There the x stream, the weight stream and the MFMAs add up
+// rather than overlap (timing variants with either load stream out of range:
+// 15 us each; MFMAs alone 8.4 us), and load depths of 2 to 6 steps, or the
+// loads interleaved with the multiplies, measured the same.
 constexpr int kWideTokens = 32;
 constexpr int kWideWaves = 4;
 constexpr int kWideMaxPer = 64;  // 64-k steps: hidden <= 4096
