@@ -404,12 +404,19 @@ struct RingOps {
         if constexpr (GATHER) {
             r.a = make_rsrc(p.a, static_cast<uint32_t>(p.a_src_rows * K * 2));
             if (!offsets) return r;
+            // All table loads first, at in-range indices, and the row bound
+            // after: a load under a branch gets a wait of its own, and every
+            // wait also waits for the ring loads already in flight.
+            int src[A_LOADS];
+#pragma unroll
+            for (int i = 0; i < A_LOADS; ++i)
+                src[i] = p.a_rows[min(row0 + (wave_ * A_LOADS + i) * 8 + lrow, p.rows - 1)];
 #pragma unroll
             for (int i = 0; i < A_LOADS; ++i) {
                 const int rr = (wave_ * A_LOADS + i) * 8 + lrow;
-                const int src = row0 + rr < row_end ? p.a_rows[row0 + rr] : -1;
-                r.a_off[i] = src >= 0 && src < p.a_src_rows
-                                 ? static_cast<uint32_t>((src * K + (pchunk ^ ring_key(rr)) * 8) * 2)
+                const int s = row0 + rr < row_end ? src[i] : -1;
+                r.a_off[i] = s >= 0 && s < p.a_src_rows
+                                 ? static_cast<uint32_t>((s * K + (pchunk ^ ring_key(rr)) * 8) * 2)
                                  : kOutOfRange;
             }
         } else {
@@ -1092,6 +1099,12 @@ __device__ __forceinline__ void ring_run_shape(const GemmParams& p, char* lds, c
     const bool chain = __builtin_amdgcn_readfirstlane(nxt.valid && nxt.variant == w.variant && k_steps >= R::SB) != 0;
     typename R::Rsrc next{};
     if (chain) next = R::tile_rsrc(p, nxt.expert, nxt.col0, nxt.row0, nxt.row_end);
+    // The hook reads the gathered offsets from their own array, not from
+    // `next`: a hook that refers to `next` keeps its buffer resources in
+    // scratch memory, and the hook's reload of them waits for the ring.
+    uint32_t next_off[R::A_LOADS];
+#pragma unroll
+    for (int i = 0; i < R::A_LOADS; ++i) next_off[i] = next.a_off[i];
     const int na = (sa + k_steps) % R::SA, nb = (sb + k_steps) % R::SB;
     auto hook = [&] {
         if (!nxt.valid) return;
@@ -1099,9 +1112,12 @@ __device__ __forceinline__ void ring_run_shape(const GemmParams& p, char* lds, c
             // Gathered rows: the next tile's offsets, formed before its k-loop;
             // otherwise they do not depend on the tile.
             if constexpr (GATHER) {
-                R(p, lds, next).prologue(k_steps, na, nb, true);
+                typename R::Rsrc res = R::tile_rsrc(p, nxt.expert, nxt.col0, nxt.row0, nxt.row_end, false);
 #pragma unroll
-                for (int i = 0; i < R::A_LOADS; ++i) a_carry[i] = next.a_off[i];
+                for (int i = 0; i < R::A_LOADS; ++i) res.a_off[i] = next_off[i];
+                R(p, lds, res).prologue(k_steps, na, nb, true);
+#pragma unroll
+                for (int i = 0; i < R::A_LOADS; ++i) a_carry[i] = next_off[i];
             } else {
                 R(p, lds, nxt.expert, nxt.col0, nxt.row0, nxt.row_end).prologue(k_steps, na, nb, true);
             }
