@@ -320,11 +320,10 @@ def _gathers(x, topk):
     """Whether the fused forward skips the packed copy, the gate/up GEMM reading
     x through the dispatch's row table. It needs the ring kernels (hidden a
     multiple of 64) and x below 2 GiB, and pays off from top-3 on: the gathered
-    GEMM waits longer on its A loads than on the just-written packed rows
-    (MFMA busy 0.67 against 0.70 at H=4096, I=14336, E=8, top-2: gate/up +2%,
-    forward +0.9%; H=1024, I=2048, E=16: gate/up +5%), while with K rows per
-    token the copy it saves grows with K (H=2048, I=1408, E=64, top-6: dispatch
-    39 -> 7 us, gate/up unchanged, forward -3.8%)."""
+    GEMM is 1-2% slower than the packed one (H=4096, I=14336, E=8: 1510 against
+    1489 us; H=1024, I=2048, E=16: +2.2%), which at top-2 costs about what the
+    copy does, while with K rows per token the copy it saves grows with K
+    (H=2048, I=1408, E=64, top-6: dispatch 39 -> 7 us, forward -3.8%)."""
     return topk >= 3 and x.shape[1] % 64 == 0 and x.numel() * x.element_size() < 2**31
 
 
