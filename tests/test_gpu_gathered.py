@@ -14,14 +14,15 @@ from x[row_src[r]] (zeros for -1). Checked here, bit for bit:
   persistent kernel (balanced row tiles at K >= 2048, plain below, chained
   tiles) and on the weight-streaming kernel (at most 128 rows), and at other
   persistent grid sizes (which change which tiles chain);
-* a table entry out of x's range reads zeros instead of faulting.
+* a table entry out of x's range reads zeros instead of faulting;
+* edge cases: no tokens, and most experts empty (skewed routing).
 """
 
 import numpy as np
 import pytest
 import torch
 
-from moe_dispatch.routing import make_transport_case
+from moe_dispatch.routing import make_case, make_transport_case
 from moe_dispatch.workspace import CudaWorkspace
 from oracle import moe_oracle as oracle
 from tests._helpers import assert_layout_equal, gpu, to_np
@@ -52,6 +53,7 @@ def _ranked(ext, ws, x, experts, topk, seed):
 
 DISPATCH_CASES = [
     # tokens, hidden, experts, topk, alignment, ranked
+    (0, 64, 8, 3, 8, False),       # no tokens: every row left as it was
     (1, 64, 8, 2, 8, False),       # one token, counted in the pack kernel
     (300, 128, 8, 2, 8, False),    # 600 assignments: counted in the pack kernel
     (4096, 64, 8, 2, 8, False),    # the counting kernel, then the pack kernel
@@ -87,8 +89,10 @@ def test_row_table_dispatch_matches_the_packed_dispatch(ext, tokens, hidden, exp
 
 
 GEMM_CASES = [
-    # tokens, hidden, intermediate, experts, topk, alignment
+    # tokens, hidden, intermediate, experts, topk, alignment[, skewed]
     (1500, 2048, 256, 8, 2, 8),    # persistent kernel, balanced row tiles (K = 2048)
+    (900, 1024, 256, 16, 3, 8, True),  # skewed: experts 0-2 hold nearly every row, most others none
+    (30, 2048, 128, 16, 4, 1, True),   # skewed (experts 0-3), weight-streaming kernel
     (1100, 1024, 384, 16, 2, 8),   # persistent kernel, plain row tiles (K = 1024), short tiles
     (2100, 4096, 136, 4, 2, 1),    # K = 4096, two column tiles (136 = 128 + 8), alignment 1
     (40, 512, 256, 8, 2, 8),       # at most 128 rows: the weight-streaming kernel
@@ -97,9 +101,13 @@ GEMM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("tokens,hidden,inter,experts,topk,alignment", GEMM_CASES)
-def test_gathered_gateup_equals_the_packed_gateup(ext, tokens, hidden, inter, experts, topk, alignment):
-    x, ids32, _, _ = make_transport_case(tokens, hidden, experts, topk, torch.bfloat16, seed=hidden + tokens)
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_gathered_gateup_equals_the_packed_gateup(ext, case):
+    tokens, hidden, inter, experts, topk, alignment = case[:6]
+    if len(case) > 6:
+        x, ids32, _, _ = make_case(tokens, hidden, experts, topk, torch.bfloat16, "skewed", seed=tokens)
+    else:
+        x, ids32, _, _ = make_transport_case(tokens, hidden, experts, topk, torch.bfloat16, seed=hidden + tokens)
     ws = CudaWorkspace(tokens, hidden, experts, topk, torch.bfloat16, alignment=alignment, extension=ext)
     ws.dispatch(x, ids32)
     ws.dispatch_rows(ids32)  # the same offsets; row_src for the gathered GEMM
