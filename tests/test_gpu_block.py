@@ -127,6 +127,17 @@ def test_small_blocks(tokens, pattern, topk):
     _check_block(MoEConfig(32, 64, 8, topk), tokens, pattern)
 
 
+@pytest.mark.parametrize("cfg,tokens", [
+    ((64, 128, 1, 1), 50),         # one expert, top-1
+    ((128, 64, 8, 8), 40),         # top-8 of 8: every token on every expert (row table)
+    ((72, 136, 12, 3), 60),        # hidden and intermediate not multiples of 64: the generic GEMM, packed rows
+    ((64, 64, 64, 8), 30),         # E=64, top-8, few tokens: most experts empty (row table)
+    ((128, 128, 4, 2, 128), 100),  # alignment 128: most packed rows are padding
+])
+def test_block_edge_configurations(cfg, tokens):
+    _check_block(MoEConfig(*cfg), tokens, seed=tokens)
+
+
 def test_config1_cpu_reference_shape():
     """T=128, H=512, I=1024, E=8, top-2 (the reference's CPU-runnable case)."""
     _check_block(MoEConfig(512, 1024, 8, 2), 128, seed=0)
