@@ -213,10 +213,11 @@ def cpu_baseline(gpu_block=None, gpu_x=None, c4_sample_tokens=64):
             "unit": "us",
             "cores": threads,
             "kind": "port",
-            "sample": "this repo's PyTorch variant of the reference block (implementation='torch': topk/softmax "
-                      "router, stable-sort transport, F.grouped_mm experts, fp32 combine) at benchmark config 1 "
-                      "(T=128 H=512 I=1024 E=8 top-2 bf16, seed 0), all 128 tokens, no scaling; median of 40 "
-                      "perf_counter_ns samples after 10 warm-ups",
+            "workload": "c1_t128",
+            "sample": "C1 (T=128 H=512 I=1024 E=8 top-2 bf16), not the bench workload: this repo's PyTorch "
+                      "variant of the reference block (implementation='torch': topk/softmax router, stable-sort "
+                      "transport, F.grouped_mm experts, fp32 combine), seed 0, all 128 tokens, no scaling; median "
+                      "of 40 perf_counter_ns samples after 10 warm-ups",
             "config": {"tokens": 128, "hidden": 512, "intermediate": 1024, "experts": 8, "topk": 2,
                        "dtype": "bf16"},
             "all_cores": runs["all_cores"],
@@ -251,12 +252,14 @@ def torch_variant_gpu(cfg, weights, x, steps, warmup):
     import torch
 
     from moe_dispatch.benchmark import measure
-    from moe_dispatch.experts import torch_backend_kind
+    from moe_dispatch.experts import backend_label, torch_backend_calls
     from moe_dispatch.layer import MoEBlock
 
     block = MoEBlock(cfg, device=x.device, implementation="torch", expert_backend="torch", weights=weights)
-    kind = torch_backend_kind(x.device)
+    before = torch_backend_calls.copy()
     stats = measure(lambda: block(x), warmup, steps)
+    # The path of the timed calls themselves (warm-up and timed forwards).
+    kind = backend_label(before, torch_backend_calls)
     del block
     torch.cuda.empty_cache()
     return {"median_us": stats["median_us"], "min_us": stats["min_us"], "gemm_backend": kind}

@@ -28,8 +28,12 @@ constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mutex;
 static void* g_scratch_address[kMaxDevices] = {};
 
-// Device address of the current device's copy of `scratch`, looked up once per device.
-static int static_scratch(void** address) {
+// Device address of the current device's copy of `scratch`, looked up once per
+// device. The lookup is a runtime call that graph capture need not allow, so a
+// first call on a device while `stream` is capturing is refused with an error
+// (make one call on each device before capturing); later calls only read the
+// cached address.
+static int static_scratch(void** address, hipStream_t stream) {
     int device = -1;
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) return fail(MOE_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(err));
@@ -37,6 +41,13 @@ static int static_scratch(void** address) {
         return fail(MOE_ERR_UNSUPPORTED, "device %d beyond the %d this build tracks", device, kMaxDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (g_scratch_address[device] == nullptr) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        err = hipStreamIsCapturing(stream, &capture);
+        if (err != hipSuccess) return fail(MOE_ERR_HIP, "hipStreamIsCapturing: %s", hipGetErrorString(err));
+        if (capture != hipStreamCaptureStatusNone)
+            return fail(MOE_ERR_UNSUPPORTED,
+                        "the first moe_dispatch_noalloc call on device %d is under graph capture: make one call "
+                        "on this device before capturing", device);
         void* ptr = nullptr;
         err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (err != hipSuccess || ptr == nullptr)
@@ -62,7 +73,7 @@ extern "C" int moe_dispatch_noalloc(const void* x, int dtype, const int32_t* ids
                 "dispatch needs %lld bytes of scratch, beyond the static %lld", (long long)need,
                 (long long)kStaticScratchBytes);
     void* address = nullptr;
-    const int rc = static_scratch(&address);
+    const int rc = static_scratch(&address, static_cast<hipStream_t>(stream));
     if (rc != MOE_OK) return rc;
     return moe_dispatch(x, dtype, ids, counts, offsets, slots, packed, inverse, address,
                         kStaticScratchBytes, tokens, hidden, experts, topk, alignment, packed_rows,

@@ -31,14 +31,25 @@ class ForwardGraph:
     replay); ``replay()`` first redoes the split, outside the graph, when the
     router weights were replaced or written in place since the split was
     taken, so every replay routes with the weights as they are. ``graph`` is
-    the underlying ``torch.cuda.CUDAGraph``: replaying it directly skips that
-    check.
+    the underlying ``torch.cuda.CUDAGraph`` (the object the reference's
+    ``capture_forward`` returns); replaying it directly skips that check, so
+    after a router-weight update it routes with the split taken before. The
+    graph's own ``reset()``, ``pool()`` and ``enable_debug_mode()`` pass through.
     """
 
     def __init__(self, block, graph, output):
         self.block = block
         self.graph = graph
         self.output = output
+
+    def reset(self):
+        self.graph.reset()
+
+    def pool(self):
+        return self.graph.pool()
+
+    def enable_debug_mode(self):
+        self.graph.enable_debug_mode()
 
     def replay(self):
         block = self.block

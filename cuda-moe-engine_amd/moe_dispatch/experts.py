@@ -6,9 +6,15 @@ per-expert ``mm`` loop where grouped_mm is unavailable). There is no Triton
 backend and no automatic fallback from ``hip``.
 """
 
+from collections import Counter
+
 import torch
 
 BACKENDS = ("auto", "torch", "hip")
+
+# Which path each torch-backend call took ("grouped_mm" or "mm_loop"), counted
+# per call so that a caller can label a timed run by the path that ran in it.
+torch_backend_calls = Counter()
 
 
 def resolve_backend(device, requested="auto"):
@@ -30,7 +36,9 @@ def _torch_grouped(x, weight, ends):
     function = getattr(torch.nn.functional, "grouped_mm", getattr(torch, "_grouped_mm", None))
     if function is not None:
         try:
-            return function(x, logical, offs=ends), "grouped_mm"
+            result = function(x, logical, offs=ends)
+            torch_backend_calls["grouped_mm"] += 1
+            return result, "grouped_mm"
         except (RuntimeError, NotImplementedError):
             pass
     # Per-expert loop (host reads the offsets).
@@ -40,6 +48,7 @@ def _torch_grouped(x, weight, ends):
         s, t = bounds[e], bounds[e + 1]
         if t > s:
             out[s:t] = x[s:t] @ logical[e]
+    torch_backend_calls["mm_loop"] += 1
     return out, "mm_loop"
 
 
@@ -68,12 +77,11 @@ def grouped_linear(x, weight, ends, *, backend, output=None, offsets=None):
     return result
 
 
-def torch_backend_kind(device):
-    """Which torch GEMM path ``grouped_linear(backend="torch")`` takes on ``device``."""
-    x = torch.zeros((8, 8), device=device, dtype=torch.bfloat16)
-    w = torch.zeros((1, 8, 8), device=device, dtype=torch.bfloat16)
-    ends = torch.tensor([8], device=device, dtype=torch.int32)
-    return _torch_grouped(x, w, ends)[1]
+def backend_label(before, after):
+    """The torch GEMM path(s) taken between two snapshots of ``torch_backend_calls``:
+    "grouped_mm", "mm_loop", "mixed" (both ran) or "none"."""
+    ran = sorted(k for k in ("grouped_mm", "mm_loop") if after[k] > before[k])
+    return ran[0] if len(ran) == 1 else ("mixed" if ran else "none")
 
 
 def swiglu_reference(projection):

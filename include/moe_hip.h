@@ -90,6 +90,10 @@ int64_t moe_router_scratch_bytes(int64_t experts, int64_t hidden);
  * router_w == NULL skips the split and uses the planes scratch already holds
  * from an earlier call with the same E and H (for callers that know the
  * router weights have not changed since; no reference counterpart).
+ * Precondition: moe_router_split, or a moe_router_fused call with router_w,
+ * wrote that scratch for this E and H. Without it the kernels read whatever
+ * the scratch holds and the ids and weights are meaningless; the call cannot
+ * tell (it reads no device memory on the host) and returns MOE_OK.
  * Calls that share one scratch must not overlap in time.
  */
 int moe_router_fused(const void* x, const float* router_w, const float* bias, int32_t* ids32,
@@ -123,8 +127,11 @@ int64_t moe_router_rank_tile(int64_t tokens, int64_t experts);
  * ids[p]} (flat order p = t*K + k; ranks holds T*K int32). moe_dispatch_ranked
  * then skips its own counting pass (one launch less per forward).
  * tile_counts_bytes >= ceil(T / tile) * E * 4; MOE_ERR_UNSUPPORTED when
- * moe_router_rank_tile returns 0. No counterpart in the reference (its router
- * and dispatch are separate passes).
+ * moe_router_rank_tile returns 0. router_w == NULL carries moe_router_fused's
+ * precondition; here meaningless ranks and tile counts would also misplace the
+ * pack's rows (moe_dispatch_ranked keeps every write inside packed_rows, but
+ * the layout is then wrong). No counterpart in the reference (its router and
+ * dispatch are separate passes).
  */
 int moe_router_fused_ranked(const void* x, const float* router_w, const float* bias, int32_t* ids32,
                             int64_t* ids64, float* weights, float* logits_out, void* scratch,
@@ -168,6 +175,9 @@ int moe_dispatch(const void* x, int dtype, const int32_t* ids, int32_t* counts, 
  * on one GPU uses that GPU's array, so calls that overlap in time on one GPU
  * (other streams or host threads) race; calls on one stream are ordered. The
  * current device must be the one the pointers and the stream belong to.
+ * The first call on each device looks the array's address up (a runtime call,
+ * not a stream operation); made while `stream` is capturing, that first call
+ * returns MOE_ERR_UNSUPPORTED, so make one call per device before capturing.
  * Arguments, results and errors are otherwise moe_dispatch's.
  */
 int moe_dispatch_noalloc(const void* x, int dtype, const int32_t* ids, int32_t* counts,
@@ -248,9 +258,13 @@ int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offse
  * Grouped gate/up GEMM with the SwiGLU epilogue fused:
  *   g = round_bf16(a[r] . gate_up[e, j]), u = round_bf16(a[r] . gate_up[e, I + j])
  *   act[r, j] = round_bf16(silu(g) * u)
- * which equals grouped_gemm followed by swiglu (reference layer.py:161-172,
- * csrc/dispatch.cu:277-292) value for value. Rows at or past offsets[E] are
- * not written. Requires hidden % 8 == 0, intermediate % 8 == 0.
+ * the computation of grouped_gemm followed by swiglu (reference
+ * layer.py:161-172, csrc/dispatch.cu:277-292). g and u are the same bf16
+ * values; the epilogue evaluates silu(g) * u as (g * u) / (1 + 2^(-g log2 e))
+ * with the hardware exp2 and reciprocal (about 1 ulp each) where moe_swiglu
+ * uses a correctly reduced exp, so a few outputs per 100 000 differ from the
+ * unfused pair by one bf16 step. Rows at or past offsets[E] are not written.
+ * Requires hidden % 8 == 0, intermediate % 8 == 0.
  */
 int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
                               const int32_t* offsets, int64_t rows, int64_t hidden,

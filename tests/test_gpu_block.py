@@ -408,8 +408,15 @@ def _check_block_sampled(cfg, tokens, bias=None, large_i=False, per_expert=6, to
     assert float(np.abs(got - dense).max()) <= MAX_ABS
     assert rel_l2(got, dense) <= (REL_L2_LARGE_I if large_i else REL_L2)
     if full_span:
+        # The expert with the fewest rows, and (when there is one) the smallest
+        # of more than 256 rows: several full-height row tiles of one expert.
         nonempty = [e for e in range(cfg.experts) if counts[e] > 0]
-        _check_expert_span(state, block, packed_rows, offsets, counts, min(nonempty, key=lambda e: counts[e]))
+        spans = {min(nonempty, key=lambda e: counts[e])}
+        tall = [e for e in nonempty if counts[e] > 256]
+        if tall:
+            spans.add(min(tall, key=lambda e: counts[e]))
+        for e in sorted(spans):
+            _check_expert_span(state, block, packed_rows, offsets, counts, e)
     return counts
 
 
@@ -425,8 +432,9 @@ def test_config3_t4096_full_size_sampled():
 
 def test_config5_full_size_zipf_skew():
     """C5: T=8192, H=2048, I=1408, E=64, top-6 with the Zipf router bias: several experts
-    get no tokens and a few take more than 15% of the assignments."""
+    get no tokens and a few take more than 15% of the assignments. Whole expert spans
+    of both GEMMs (the gate/up one gathering its rows from x) are checked too."""
     cfg = MoEConfig(2048, 1408, 64, 6)
-    counts = _check_block_sampled(cfg, 8192, bias=oracle.zipf_bias(64))
+    counts = _check_block_sampled(cfg, 8192, bias=oracle.zipf_bias(64), full_span=True)
     assert int((counts == 0).sum()) >= 3
     assert int((counts > 0.15 * 8192 * 6).sum()) >= 2

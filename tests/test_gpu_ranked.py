@@ -101,3 +101,48 @@ def test_shapes_without_a_ranked_route_keep_the_counting_pass(ext):
     ids = torch.zeros(8192, 6, device="cuda", dtype=torch.int32)
     with pytest.raises(RuntimeError, match="no ranked route"):
         ws.dispatch_ranked(x, ids)
+
+
+@pytest.mark.parametrize("tokens,hidden,experts,topk", [(4096, 4096, 8, 2), (4096, 1024, 16, 2)])
+def test_benchmark_routing_on_every_token(ext, tokens, hidden, experts, topk):
+    """The ranked route the block's forward takes at C4 T=4096 (H=4096, E=8, top-2;
+    the timed benchmark) and C3 T=4096 (H=1024, E=16), over every token: the
+    logits are within the fp32 bound of the float64 logits, the ids equal the
+    oracle's selection on the kernel's own logits bit for bit (weights within
+    2e-6), the call without logits (as the forward makes it) selects the same ids
+    and weights, and ranks and tile counts equal their definition."""
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(tokens, hidden, device="cuda", generator=gen).bfloat16()
+    w = torch.randn(experts, hidden, device="cuda", generator=gen) / hidden**0.5
+    bias = torch.zeros(experts, device="cuda")
+    tile = ext.router_rank_tile(tokens, experts)
+    assert tile == 16
+    tables = -(-tokens // tile) * experts
+
+    def run(with_logits):
+        shape = (tokens, topk)
+        out = [torch.empty(shape, device="cuda", dtype=torch.int32),
+               torch.empty(shape, device="cuda", dtype=torch.int64),
+               torch.empty(shape, device="cuda"),
+               torch.full((tokens * topk,), -7, device="cuda", dtype=torch.int32),
+               torch.full((tables,), -7, device="cuda", dtype=torch.int32)]
+        logits = torch.empty(tokens, experts, device="cuda") if with_logits else None
+        ext.router_fused_ranked_out(x, w, bias, *out, logits=logits)
+        return out, logits
+
+    (ids32, ids64, weights, ranks, tile_counts), logits = run(True)
+    got_logits = to_np(logits)
+    ref_logits = oracle.router_logits(to_np(x), to_np(w))
+    scale = np.linalg.norm(to_np(x).astype(np.float64), axis=1)[:, None] * np.linalg.norm(to_np(w), axis=1)[None, :]
+    assert np.all(np.abs(got_logits - ref_logits) <= 1e-6 * scale + 1e-7)
+    ids_ref, w_ref, _ = oracle.topk_route(got_logits, to_np(bias), topk)
+    np.testing.assert_array_equal(to_np(ids32), ids_ref)
+    np.testing.assert_array_equal(to_np(ids64), ids_ref.astype(np.int64))
+    np.testing.assert_allclose(to_np(weights), w_ref, rtol=2e-6, atol=2e-6)
+    plain, none = run(False)
+    assert none is None
+    for a, b in zip(plain, (ids32, ids64, weights, ranks, tile_counts)):
+        assert torch.equal(a, b)
+    r_ref, c_ref = _tile_reference(ids_ref, tile, experts)
+    np.testing.assert_array_equal(to_np(ranks), r_ref)
+    np.testing.assert_array_equal(to_np(tile_counts), c_ref)
