@@ -698,16 +698,8 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
     second_half(va[1] + a_first, vb[1] + b_first, More{}, NoLoads{}, none);
     first_half(vb[1] + b_first, NoLoads{}, none);
     int sa = sa0, sb = sb0;  // ring slots of stage u
-    for (int u = 0; u + 1 < k_steps; ++u) {
-        const int na = sa + 1 == SA ? 0 : sa + 1;
-        const int nb = sb + 1 == SB ? 0 : sb + 1;
-        // Stages past this tile's last: the next tile's first ones when
-        // chained, else this tile's last one again.
-        const bool a_next = chain && u + SA >= k_steps;
-        const bool b_next = chain && u + SB >= k_steps;
-        const Refill rf{a_next ? u + SA - k_steps : min(u + SA, k_steps - 1), sa,
-                        b_next ? u + SB - k_steps : min(u + SB, k_steps - 1), sb,
-                        a_next ? next.a : ops.rsrc_a, b_next ? next.b : ops.rsrc_b, a_next};
+    // The window after the barrier that precedes stage u+1's first read.
+    auto window = [&](const Refill& rf, int na, int nb) {
         const uint32_t a0 = va[0] + na * A_STAGE, a1 = va[1] + na * A_STAGE;
         const uint32_t b0 = vb[0] + nb * B_STAGE, b1 = vb[1] + nb * B_STAGE;
         fence();
@@ -720,6 +712,33 @@ __device__ __forceinline__ void ring_tile(const GemmParams& p, char* lds, int ex
         first_half(b0, std::integral_constant<int, 1>{}, rf);
         second_half(a1, b1, More{}, std::integral_constant<int, 2>{}, rf);
         first_half(b1, std::integral_constant<int, 3>{}, rf);
+    };
+    // With one wave per SIMD, every scalar instruction between two MFMAs takes
+    // an issue slot of the wave, and a burst of them before the barrier left
+    // the MFMA pipe idle (the refill's resource selects: about 40 scalar
+    // instructions per stage). So the stages whose refills come from this
+    // tile, at stages u+SA and u+SB, run in a loop of their own without
+    // selects; only the last SB-1 windows (clamped stages, or the next tile's
+    // first stages when chained) compute their refill in full.
+    int u = 0;
+    for (; u < k_steps - SB; ++u) {
+        const int na = sa + 1 == SA ? 0 : sa + 1;
+        const int nb = sb + 1 == SB ? 0 : sb + 1;
+        window(Refill{u + SA, sa, u + SB, sb, ops.rsrc_a, ops.rsrc_b, false}, na, nb);
+        sa = na;
+        sb = nb;
+    }
+    for (; u + 1 < k_steps; ++u) {
+        const int na = sa + 1 == SA ? 0 : sa + 1;
+        const int nb = sb + 1 == SB ? 0 : sb + 1;
+        // Stages past this tile's last: the next tile's first ones when
+        // chained, else this tile's last one again.
+        const bool a_next = chain && u + SA >= k_steps;
+        const bool b_next = chain && u + SB >= k_steps;
+        window(Refill{a_next ? u + SA - k_steps : min(u + SA, k_steps - 1), sa,
+                      b_next ? u + SB - k_steps : min(u + SB, k_steps - 1), sb,
+                      a_next ? next.a : ops.rsrc_a, b_next ? next.b : ops.rsrc_b, a_next},
+               na, nb);
         sa = na;
         sb = nb;
     }
