@@ -42,6 +42,12 @@ CASES = [
     (1000, 96, 5, 3, 128, torch.float32, True),
     (2049, 40, 64, 8, 1, torch.float16, True),
     (130, 3, 4, 2, 16, torch.bfloat16, True),
+    # Just past the pack kernel's own ranking (1024 assignments), experts 8-15
+    # in use, the largest K, the scalar path, and an odd assignment count
+    (513, 64, 16, 2, 8, torch.bfloat16, True),
+    (2048, 64, 16, 8, 1, torch.float16, True),
+    (777, 3, 4, 2, 16, torch.bfloat16, True),
+    (3277, 32, 8, 5, 8, torch.bfloat16, True),
 ]
 
 
@@ -73,7 +79,9 @@ def test_combine_k2_matches_torch_weighted_sum_exactly(ext):
     torch.testing.assert_close(ws.output, expected, rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("tokens", [6, 700])  # pack ranks the ids itself up to 1024 assignments
+# 6 tokens: the pack kernel ranks every id itself (up to 1024 assignments);
+# 700: the counting kernel first
+@pytest.mark.parametrize("tokens", [6, 700])
 def test_out_of_range_ids_are_masked(ext, tokens):
     x = torch.randn(tokens, 32, device="cuda").bfloat16()
     if tokens == 6:
@@ -110,6 +118,20 @@ def test_dispatch_and_combine_are_deterministic(ext, alignment):
         results.append([raw_bits(t) for t in (ws.packed, ws.inverse, ws.slots, ws.offsets, ws.output)])
     for a, b in zip(*results):
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("experts", [8, 16])
+def test_one_expert_takes_every_assignment(ext, experts):
+    """16384 assignments to one expert (the last): every chunk's count lands in
+    one column of the count table, and one expert's span holds every row."""
+    tokens, topk, hidden = 2048, 8, 64
+    x = torch.randn(tokens, hidden, device="cuda").bfloat16()
+    ids = torch.full((tokens, topk), experts - 1, device="cuda", dtype=torch.int32)
+    ws = CudaWorkspace(tokens, hidden, experts, topk, torch.bfloat16, alignment=8, extension=ext)
+    ws.dispatch(x, ids)
+    layout = oracle.dispatch_layout(to_np(ids), experts, 8)
+    assert_layout_equal(ws, layout, tokens, topk, experts)
+    assert_packed_equal(ws.packed, x, layout, topk)
 
 
 def test_full_transport_configuration_bit_exact(ext):
