@@ -22,11 +22,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              kRsrcWord3);
 }
 
+// soffset is wave-uniform at every call; readfirstlane states it, so that the
+// compiler keeps it in an SGPR. Where it could not prove that (stage indices
+// clamped with min() in the prologues), it wrapped each load in a waterfall
+// loop of about ten instructions.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst, uint32_t voffset,
                                       uint32_t soffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rsrc, (__attribute__((address_space(3))) void*)(lds_dst), 16, voffset, soffset,
-        0, 0);
+        rsrc, (__attribute__((address_space(3))) void*)(lds_dst), 16, voffset,
+        __builtin_amdgcn_readfirstlane(soffset), 0, 0);
 }
 
 // s_waitcnt vmcnt(VM) lgkmcnt(LGKM) (gfx9 encoding: vmcnt[3:0] in bits 3:0 and
