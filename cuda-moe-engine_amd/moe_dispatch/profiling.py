@@ -1,4 +1,6 @@
-"""Summaries of rocprofv3 counter collections for the expert GEMMs (MFMA utilisation, clock).
+"""Summaries of rocprofv3 output: counter collections for the expert GEMMs
+(MFMA utilisation, clock, stalls, memory) and kernel traces (steady-state
+launch times).
 
 ``python -m moe_dispatch.profiling <dir>/run_counter_collection.csv`` prints a
 markdown table with one line per run of consecutive launches of one kernel
@@ -13,7 +15,15 @@ markdown table with one line per run of consecutive launches of one kernel
   FLOP, padding rows included (the algorithmic FLOP excludes them);
 * the fraction of CU cycles with a wave resident (``SQ_BUSY_CU_CYCLES``).
 
-Each counter appears only if it was collected. Standard library only.
+Each counter appears only if it was collected; ``--raw`` adds every other
+collected counter, normalised where its unit is known (quad-cycle wave
+counters and per-SIMD busy counters over SIMD cycles, per-CU LDS and TA stall
+counters over CU cycles, ``TCP_TCC_READ_REQ_LATENCY`` as cycles per request).
+
+``python -m moe_dispatch.profiling --trace <dir>/run_kernel_trace.csv`` prints
+the mean and minimum duration of the last N launches of each kernel (the
+steady state of a timed loop) and, with ``--stats <dir>/run_kernel_stats.csv``,
+rocprofv3's table of all launches. Standard library only.
 """
 
 from __future__ import annotations
@@ -53,14 +63,16 @@ def runs(items, keep=None, last=None):
     average only the last `last` launches of each run (the steady state)."""
     groups = []
     for name, dur, counters in items:
-        if keep and not re.search(keep, name):
-            continue
+        # Runs are cut by any other kernel, kept or not: two runs of one kernel
+        # with other work between them stay apart.
         if groups and groups[-1][0] == name:
             groups[-1][1].append((dur, counters))
         else:
             groups.append((name, [(dur, counters)]))
     out = []
     for name, members in groups:
+        if keep and not re.search(keep, name):
+            continue
         chosen = members[-last:] if last else members
         n = len(chosen)
         dur = sum(d for d, _ in chosen) / n
@@ -79,27 +91,112 @@ def runs(items, keep=None, last=None):
                 row["cu_busy"] = mean["SQ_BUSY_CU_CYCLES"] / (CUS * cycles)
         if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in mean:
             row["mfma_flop"] = mean["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512
+        row["raw"] = _normalised(mean, gui / XCDS if gui else None)
         out.append(row)
     return out
 
 
-def markdown(rows):
+# Wave counters in quad-cycles summed over the SIMDs; per-SIMD busy counters;
+# per-CU counters.
+_QUAD_SIMD = ("SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_ANY",
+              "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_VALU")
+_PER_CU = ("SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_DATA_FIFO_FULL", "SQ_LDS_CMD_FIFO_FULL",
+           "SQ_VMEM_TA_ADDR_FIFO_FULL", "SQ_VMEM_TA_CMD_FIFO_FULL")
+_SKIP = ("GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16")
+
+
+def _normalised(mean, cycles):
+    out = {}
+    for name, value in mean.items():
+        if name in _SKIP:
+            continue
+        key = name[:-4] if name.endswith("_sum") else name
+        if cycles and name in _QUAD_SIMD:
+            out[key + "/cyc"] = value * 4 / (SIMDS * cycles)
+        elif cycles and name in _PER_CU:
+            out[key + "/cyc"] = value / (CUS * cycles)
+        elif key == "TCP_TCC_READ_REQ_LATENCY":
+            req = mean.get("TCP_TCC_READ_REQ_sum", mean.get("TCP_TCC_READ_REQ"))
+            out["TCC_READ_LATENCY_cyc"] = value / req if req else float("nan")
+        else:
+            out[key] = value
+    return out
+
+
+def trace_launches(path):
+    """(kernel, duration_us) in dispatch order from a rocprofv3 kernel-trace CSV."""
+    rows = []
+    with open(path, newline="") as f:
+        for rec in csv.DictReader(f):
+            dur = (int(rec["End_Timestamp"]) - int(rec["Start_Timestamp"])) / 1000.0
+            rows.append((int(rec.get("Dispatch_Id", len(rows))), _short(rec["Kernel_Name"]), dur))
+    rows.sort()
+    return [(name, dur) for _, name, dur in rows]
+
+
+def steady_state(items, last=10, keep=None):
+    """Per kernel (first-launch order): launches, mean and min of the last `last` launches."""
+    by = OrderedDict()
+    for name, dur in items:
+        if keep and not re.search(keep, name):
+            continue
+        by.setdefault(name, []).append(dur)
+    out = []
+    for name, durs in by.items():
+        tail = durs[-last:]
+        out.append({"kernel": name, "launches": len(durs), "mean_us": sum(tail) / len(tail), "min_us": min(tail)})
+    return out
+
+
+def stats_table(path, top=15):
+    """rocprofv3's kernel stats CSV as a markdown table (the `top` kernels by time)."""
+    with open(path, newline="") as f:
+        recs = list(csv.DictReader(f))
+    recs.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    lines = ["| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
+    for r in recs[:top]:
+        lines.append("| `{}` | {} | {:.2f} | {:.2f} | {:.2f} | {:.2f} |".format(
+            _short(r["Name"])[:90], r["Calls"], float(r["AverageNs"]) / 1000, float(r["MinNs"]) / 1000,
+            float(r["MaxNs"]) / 1000, float(r["Percentage"])))
+    return "\n".join(lines)
+
+
+def markdown(rows, raw=False):
     cols = [("kernel", "{}"), ("launches", "{}"), ("averaged", "{}"), ("us", "{:.1f}"), ("clock_ghz", "{:.3f}"),
             ("mfma_busy", "{:.3f}"), ("cu_busy", "{:.3f}"), ("mfma_flop", "{:.4g}")]
     present = [(c, f) for c, f in cols if any(c in r for r in rows)]
-    lines = ["| " + " | ".join(c for c, _ in present) + " |", "|" + "---|" * len(present)]
+    extra = sorted({k for r in rows for k in r.get("raw", {})}) if raw else []
+    lines = ["| " + " | ".join([c for c, _ in present] + extra) + " |", "|" + "---|" * (len(present) + len(extra))]
     for r in rows:
-        lines.append("| " + " | ".join(f.format(r[c]) if c in r else "" for c, f in present) + " |")
+        cells = [f.format(r[c]) if c in r else "" for c, f in present]
+        cells += ["{:.4g}".format(r["raw"][k]) if k in r.get("raw", {}) else "" for k in extra]
+        lines.append("| " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
+def trace_markdown(rows):
+    lines = ["| kernel | launches | mean us (last N) | min us (last N) |", "|---|---|---|---|"]
+    for r in rows:
+        lines.append("| `{}` | {} | {:.2f} | {:.2f} |".format(r["kernel"], r["launches"], r["mean_us"], r["min_us"]))
     return "\n".join(lines)
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("csv", help="rocprofv3 run_counter_collection.csv")
+    ap.add_argument("csv", help="rocprofv3 run_counter_collection.csv (or, with --trace, run_kernel_trace.csv)")
     ap.add_argument("--keep", default=None, help="regex of kernel names to keep")
     ap.add_argument("--last", type=int, default=None, help="average the last N launches of each run")
+    ap.add_argument("--raw", action="store_true", help="also every other collected counter, normalised")
+    ap.add_argument("--trace", action="store_true", help="the csv is a kernel trace: steady-state launch times")
+    ap.add_argument("--stats", default=None, help="with --trace: run_kernel_stats.csv for the all-launches table")
     args = ap.parse_args(argv)
-    print(markdown(runs(launches(args.csv), args.keep, args.last)))
+    if args.trace:
+        print(trace_markdown(steady_state(trace_launches(args.csv), args.last or 10, args.keep)))
+        if args.stats:
+            print()
+            print(stats_table(args.stats))
+        return 0
+    print(markdown(runs(launches(args.csv), args.keep, args.last), args.raw))
     return 0
 
 
