@@ -99,6 +99,10 @@ SCHEDULE_CASES = [
     # (experts of 304, 424, 520 and 704 rows), 1040 rows as five of 224, and a
     # phase-2 tile of 104 rows
     ([300, 420, 520, 700, 1034, 100], 8, 136, 2048, True, (8, 24, 64)),
+    # experts of more than 8 row tiles (2600 and 4100 rows): their phase-1 tiles
+    # run in groups of at most 8 row tiles
+    ([2600, 300, 4100, 40], 8, 512, 128, False, (8, 24)),
+    ([2600, 300, 4100, 40], 8, 384, 128, True, (8, 24)),
 ]
 
 

@@ -248,3 +248,32 @@ def test_measured_shapes_get_the_intended_plans():
     # No short tiles: phase 1 alone, as before.
     pl = ring_plan(*phase_counts([1024] * 8, 8, 112), 256, False)
     assert (pl["rounds"], pl["rest"]["blocks"]) == (0, 3584)
+
+
+def phase1_tile(rel, mf, n_tiles):
+    """ring_locate's phase-1 mapping: an expert's row tiles in groups of at most 8
+    (balanced heights), column tiles fastest inside a group, row tiles fastest
+    inside a column. Returns (column tile, row tile)."""
+    groups = (mf + 7) // 8
+    hg = -(-mf // groups)
+    full = hg * n_tiles
+    g = rel // full
+    height = min(hg, mf - g * hg)
+    r = rel - g * full
+    n = r // height
+    return n, g * hg + (r - n * height)
+
+
+def test_phase1_tile_order_covers_each_tile_once_in_groups_of_eight():
+    for mf in range(1, 70):
+        for n_tiles in (1, 2, 3, 7, 8, 11, 16, 112):
+            tiles = [phase1_tile(rel, mf, n_tiles) for rel in range(mf * n_tiles)]
+            assert sorted(tiles) == [(n, m) for n in range(n_tiles) for m in range(mf)]
+            if mf <= 8:  # the plain order: row tiles fastest
+                assert tiles == [(rel // mf, rel % mf) for rel in range(mf * n_tiles)]
+    # 32 row tiles, 11 column tiles (H=2048, I=1408 gate/up): any 32 consecutive
+    # tiles span at most 8 row tiles (four groups of 8); the plain order spanned 32.
+    tiles = [phase1_tile(rel, 32, 11) for rel in range(32 * 11)]
+    for start in range(0, len(tiles) - 32, 32):
+        window = tiles[start:start + 32]
+        assert len({m for _, m in window}) <= 16 and len({n for n, _ in window}) >= 2
