@@ -57,12 +57,17 @@ def sample_statistics(samples):
             "min_us": min(samples)}
 
 
+# Package modules that never run inside a measurement: profiling.py summarises
+# profiler output files afterwards.
+OFFLINE_MODULES = ("profiling.py",)
+
+
 def source_files():
     """What a measurement depends on: kernel sources, the ABI header and the package modules."""
     files = sorted(CSRC_DIR.glob("*.hip")) + sorted(CSRC_DIR.glob("*.h"))
     if HEADER.is_file():
         files.append(HEADER)
-    files += sorted(PACKAGE_DIR.glob("*.py"))
+    files += sorted(f for f in PACKAGE_DIR.glob("*.py") if f.name not in OFFLINE_MODULES)
     return [f for f in files if f.is_file()]
 
 

@@ -20,10 +20,11 @@ collected counter, normalised where its unit is known (quad-cycle wave
 counters and per-SIMD busy counters over SIMD cycles, per-CU LDS and TA stall
 counters over CU cycles, ``TCP_TCC_READ_REQ_LATENCY`` as cycles per request).
 
-``python -m moe_dispatch.profiling --trace <dir>/run_kernel_trace.csv`` prints
-the mean and minimum duration of the last N launches of each kernel (the
-steady state of a timed loop) and, with ``--stats <dir>/run_kernel_stats.csv``,
-rocprofv3's table of all launches. Standard library only.
+``python -m moe_dispatch.profiling --trace <dir>/run_kernel_trace.csv`` prints,
+per kernel, the mean and minimum duration of the last N launches of its longest
+run of back-to-back launches (the steady state of a timed replay of repeated
+calls) and, with ``--stats <dir>/run_kernel_stats.csv``, rocprofv3's table of
+all launches. Standard library only.
 """
 
 from __future__ import annotations
@@ -135,16 +136,35 @@ def trace_launches(path):
 
 
 def steady_state(items, last=10, keep=None):
-    """Per kernel (first-launch order): launches, mean and min of the last `last` launches."""
+    """Per kernel (first-launch order): its launches, the length of its longest run of
+    back-to-back launches (no other kernel between them: a call replayed from a graph of
+    repeated calls), and the mean and min of the last `last` launches of that run (the
+    last such run where several are equally long). Launches after the run (a later
+    forward) do not enter the mean. A kernel never launched twice in a row averages its
+    last `last` launches."""
     by = OrderedDict()
+    prev = None
     for name, dur in items:
         if keep and not re.search(keep, name):
+            prev = name
             continue
-        by.setdefault(name, []).append(dur)
+        entry = by.setdefault(name, {"launches": 0, "runs": []})
+        entry["launches"] += 1
+        if prev == name:
+            entry["runs"][-1].append(dur)
+        else:
+            entry["runs"].append([dur])
+        prev = name
     out = []
-    for name, durs in by.items():
-        tail = durs[-last:]
-        out.append({"kernel": name, "launches": len(durs), "mean_us": sum(tail) / len(tail), "min_us": min(tail)})
+    for name, entry in by.items():
+        longest = max(len(r) for r in entry["runs"])
+        if longest > 1:
+            chosen = [r for r in entry["runs"] if len(r) == longest][-1]
+        else:
+            chosen = [r[0] for r in entry["runs"]]
+        tail = chosen[-last:]
+        out.append({"kernel": name, "launches": entry["launches"], "run": longest,
+                    "mean_us": sum(tail) / len(tail), "min_us": min(tail)})
     return out
 
 
@@ -175,9 +195,11 @@ def markdown(rows, raw=False):
 
 
 def trace_markdown(rows):
-    lines = ["| kernel | launches | mean us (last N) | min us (last N) |", "|---|---|---|---|"]
+    lines = ["| kernel | launches | longest back-to-back run | mean us (its last N) | min us (its last N) |",
+             "|---|---|---|---|---|"]
     for r in rows:
-        lines.append("| `{}` | {} | {:.2f} | {:.2f} |".format(r["kernel"], r["launches"], r["mean_us"], r["min_us"]))
+        lines.append("| `{}` | {} | {} | {:.2f} | {:.2f} |".format(r["kernel"], r["launches"], r["run"], r["mean_us"],
+                                                                    r["min_us"]))
     return "\n".join(lines)
 
 
@@ -185,7 +207,8 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("csv", help="rocprofv3 run_counter_collection.csv (or, with --trace, run_kernel_trace.csv)")
     ap.add_argument("--keep", default=None, help="regex of kernel names to keep")
-    ap.add_argument("--last", type=int, default=None, help="average the last N launches of each run")
+    ap.add_argument("--last", type=int, default=None,
+                    help="average the last N launches of each run (with --trace: of each kernel's longest run)")
     ap.add_argument("--raw", action="store_true", help="also every other collected counter, normalised")
     ap.add_argument("--trace", action="store_true", help="the csv is a kernel trace: steady-state launch times")
     ap.add_argument("--stats", default=None, help="with --trace: run_kernel_stats.csv for the all-launches table")

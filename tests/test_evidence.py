@@ -155,6 +155,7 @@ def test_source_hashes_cover_kernels_header_and_modules():
     hashes = evidence.source_hashes()
     assert {"gemm.hip", "dispatch.hip", "router.hip", "abi.hip", "moe_common.h", "moe_hip.h",
             "evidence.py", "layer.py"} <= set(hashes)
+    assert "profiling.py" not in hashes  # summarises profiler output after a run
     assert all(len(v) == 64 for v in hashes.values())
 
 
