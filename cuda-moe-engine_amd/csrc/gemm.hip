@@ -64,6 +64,18 @@ struct GemmParams {
 // load returns zero and moves no data.
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
+// Expert e's first row and row count from the offsets, clamped to [0, rows].
+// The offsets are read from the caller's device memory: values past the
+// buffer (a caller's mistake: counts that disagree with the rows) would
+// otherwise size the persistent kernels' tile walks (garbage counts once made
+// one launch walk empty tiles for a second). Valid offsets are unchanged.
+__device__ __forceinline__ void expert_rows(const GemmParams& p, int e, int& off, int& span) {
+    const int64_t lo = min(max(static_cast<int64_t>(p.offsets[e]), int64_t{0}), p.rows);
+    const int64_t hi = min(max(static_cast<int64_t>(p.offsets[e + 1]), lo), p.rows);
+    off = static_cast<int>(lo);
+    span = static_cast<int>(hi - lo);
+}
+
 // 16-byte chunk c of LDS row r lives at physical chunk c ^ f(r), f(r) = (r ^ (r >> 3)) & 7.
 // A 16-byte read is serviced 16 lanes at a time across 64 four-byte banks (two
 // 128-byte rows); with this f, 16 consecutive rows at one logical chunk hit 16
@@ -993,10 +1005,7 @@ __device__ __forceinline__ RingTable ring_table(const GemmParams& p, bool balanc
     const int lane = threadIdx.x & 63;
     t.off = 0;
     t.span = 0;
-    if (lane < p.experts) {
-        t.off = p.offsets[lane];
-        t.span = max(p.offsets[lane + 1] - t.off, 0);
-    }
+    if (lane < p.experts) expert_rows(p, lane, t.off, t.span);
     const int tiles = (t.span + 255) / 256;
     t.mf = balanced ? (t.span > 128 ? tiles : 0) : t.span / 256 + ((t.span % 256) > 128 ? 1 : 0);
     t.c1 = t.mf * p.n_tiles;
@@ -1293,10 +1302,7 @@ __global__ __launch_bounds__(kRingThreads) void grouped_gemm_decode_kernel(GemmP
     // and its first tile. Tiles go expert by expert, column tile by column
     // tile, row tiles fastest (so an expert's row tiles share a weight slab).
     int off = 0, span = 0;
-    if (lane < p.experts) {
-        off = p.offsets[lane];
-        span = max(p.offsets[lane + 1] - off, 0);
-    }
+    if (lane < p.experts) expert_rows(p, lane, off, span);
     const int m_tiles = (span + MAX_ROWS - 1) / MAX_ROWS;
     const int count = m_tiles * p.n_tiles;
     const int incl = wave_inclusive_sum(count);

@@ -145,6 +145,35 @@ def test_schedule_does_not_change_results(ext, counts, alignment, n, k, swiglu, 
     assert rel_l2(got[:used], ref) < 3e-3
 
 
+# rows of A, ascending offsets as given (past the rows, negative), the same clamped to [0, rows]
+CLAMP_CASES = [
+    (600, [0, 100, 2_000_000_000, 2_147_483_000], [0, 100, 600, 600]),
+    (600, [-50, 300, 350, 900], [0, 300, 350, 600]),
+    (100, [0, 40, 1_000_000, 1_000_000], [0, 40, 100, 100]),  # at most 128 rows: the weight-streaming kernel
+]
+
+
+@pytest.mark.parametrize("swiglu", [False, True])
+@pytest.mark.parametrize("rows,given,clamped", CLAMP_CASES)
+def test_offsets_outside_the_rows_act_as_clamped(ext, rows, given, clamped, swiglu):
+    """Offsets read from device memory are clamped to [0, rows] before they size
+    the tile walk: offsets past the rows (counts that disagree with the buffer)
+    give the output of the clamped offsets, promptly, and no row past them is
+    written."""
+    n, k = 256, 256
+    g = torch.Generator(device="cuda").manual_seed(rows + 7)
+    a = torch.randn(rows, k, device="cuda", generator=g).bfloat16()
+    w = (torch.randn(3, 2 * n if swiglu else n, k, device="cuda", generator=g) / k**0.5).bfloat16()
+    run = ext.gateup_swiglu_out if swiglu else ext.grouped_gemm_out
+    outs = []
+    for off in (given, clamped):
+        out = torch.full((rows, n), 5.0, device="cuda").bfloat16()
+        run(a, w, torch.tensor(off, device="cuda", dtype=torch.int32), out)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+
+
 GATEUP_CASES = [
     # counts, alignment, hidden, intermediate
     ([5, 0, 37, 300, 8, 0, 1, 64], 8, 64, 128),
