@@ -418,7 +418,9 @@ def gemm_study(block, x, args):
     """Expert GEMMs beside hipBLASLt and the same kernels on a dense problem (one JSON line).
 
     For the configuration's real routing: the gate/up (+ SwiGLU) and down grouped
-    GEMMs; torch.matmul (hipBLASLt) on dense bf16 GEMMs of the same total shape
+    GEMMs (where the forward gathers the gate/up GEMM's rows from x, the packed
+    gate/up GEMM on the packed copy of the same rows, then the gathered one);
+    torch.matmul (hipBLASLt) on dense bf16 GEMMs of the same total shape
     (M = assignments); this build's kernels on one expert holding all M rows (no
     short row tiles); and the grouped GEMMs again with zero weights, which keeps
     the schedule and the data movement but not the multiplier activity. Run it
@@ -444,8 +446,17 @@ def gemm_study(block, x, args):
 
     with torch.inference_mode():
         block(x)
+        gathered = block._launches[(x.shape[0], x.device)].gathered
+        if gathered:
+            # The forward wrote the row table only: the packed copy of the same
+            # layout (same offsets) for the packed kernel.
+            ids32, ids64, _ = block._route_buffers[(x.shape[0], x.device)]
+            t.dispatch(x, ids32, ids64)
         row("gateup_swiglu", lambda: ext.gateup_swiglu_out(t.packed, block.gate_up_weight, t.offsets,
                                                            state.activated), flop_gu)
+        if gathered:
+            row("gateup_swiglu_gathered", lambda: ext.gateup_swiglu_gathered_out(
+                x, t.row_src, block.gate_up_weight, t.offsets, state.activated), flop_gu)
         row("down", lambda: ext.grouped_gemm_out(state.activated, block.down_weight, t.offsets,
                                                  state.expert_output), flop_dn)
         gen = torch.Generator(device=x.device).manual_seed(3)
