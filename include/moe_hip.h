@@ -247,7 +247,10 @@ int moe_swiglu(const void* projection, int dtype, const int32_t* valid_rows, voi
  * Grouped bf16 GEMM on MFMA: for every expert e and row r in
  * [offsets[e], offsets[e+1]):  c[r, :] = round_bf16(a[r, :] . b[e]^T)
  * with fp32 accumulation. a [rows, k], b [E, n, k], c [rows, n].
- * Rows at or past offsets[E] are not written.
+ * Rows at or past offsets[E] are not written. The offsets are read on the
+ * device and not validated: whatever they hold, only rows [0, rows) of a and
+ * c are accessed, and the persistent kernels clamp each span to [0, rows]
+ * before they size their tile walk (so offsets past the buffer cost no time).
  * Replaces grouped_linear -> grouped_mm (reference src/moe_dispatch/experts.py:21-35,
  * _triton_gemm.py:16-104; ENDS = offsets[1:]). Requires n % 8 == 0, k % 8 == 0.
  */
