@@ -24,7 +24,9 @@ _ID_DTYPES = (torch.int32, torch.int64)
 
 @dataclass(frozen=True)
 class PackedTokens:
-    """Views into a workspace. Clone tensors before reusing that workspace if retaining them."""
+    """The packed rows, inverse map, counts and offsets of one dispatch, as views of
+    its workspace's buffers: the next call on that workspace overwrites them, so
+    clone what must outlive it."""
 
     packed: torch.Tensor
     inverse: torch.Tensor
@@ -63,7 +65,11 @@ def validate_inputs(x, expert_ids, experts):
 
 @torch.inference_mode()
 def dispatch(x, expert_ids, experts, *, workspace=None, vectorized=True, alignment=1):
-    """Pack routed tokens by expert. Bounds checks synchronize; validate once for hot loops."""
+    """Group each token's K routed copies by expert (the reference's ``dispatch``).
+
+    The expert-id range check reads the ids back to the host and so waits for
+    the stream; loops that call this repeatedly on checked ids should call the
+    workspace's ``dispatch`` instead."""
     validate_inputs(x, expert_ids, experts)
     if not x.is_cuda:
         raise RuntimeError("dispatch requires a GPU; TorchWorkspace provides the CPU reference")
@@ -95,7 +101,9 @@ _COMBINE_RULES = (
 
 @torch.inference_mode()
 def combine(expert_output, batch, weights):
-    """Weighted gather/reduction; returns a reusable output view and accumulates in FP32."""
+    """Sum each token's K expert rows weighted by its routing weights, in fp32 and
+    in k order, into the workspace's output buffer (returned as a view that the
+    next combine on that workspace overwrites)."""
     for holds, error, message in _COMBINE_RULES:
         if not holds(expert_output, batch, weights):
             raise error(message)

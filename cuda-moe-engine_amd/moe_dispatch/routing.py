@@ -1,4 +1,4 @@
-"""Seeded synthetic routed-token inputs, generated outside timed regions.
+"""Synthetic routed tokens from one seeded generator (made before any timing starts).
 
 Restates ``make_case`` (reference ``src/moe_dispatch/routing.py:6-17``): from
 one seeded generator, x ~ N(0,1) in the requested dtype, then fp32 logits
