@@ -411,8 +411,10 @@ struct RingOps {
         const int lrow = lane >> 3;
         const int pchunk = lane & 7;
         Rsrc r;
+        // The expert's weight rows from col0 on (none when col0 is past them:
+        // the range must not wrap).
         r.b = make_rsrc(p.b + (static_cast<int64_t>(expert) * p.nb + col0) * K,
-                        static_cast<uint32_t>((p.nb - col0) * K * 2));
+                        static_cast<uint32_t>(max<int64_t>(p.nb - col0, 0) * K * 2));
         if constexpr (GATHER) {
             r.a = make_rsrc(p.a, static_cast<uint32_t>(p.a_src_rows * K * 2));
             if (!offsets) return r;
@@ -1093,6 +1095,10 @@ __device__ __forceinline__ RingWork ring_locate(const GemmParams& p, const RingT
         w.col0 = static_cast<int64_t>(n_tile) * 256 + (s.piece - 4) * 64;
         w.variant += 6;
     }
+    // A piece of the last column tile can start at or past the last output
+    // column (N < 256, or a last tile of at most 192 columns): it has no
+    // work, and its weight rows would start past the expert's.
+    if (w.col0 >= p.n_out) return w;
     w.expert = e;
     w.valid = true;
     return w;

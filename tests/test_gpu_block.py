@@ -133,6 +133,7 @@ def test_small_blocks(tokens, pattern, topk):
     ((72, 136, 12, 3), 60),        # hidden and intermediate not multiples of 64: the generic GEMM, packed rows
     ((64, 64, 64, 8), 30),         # E=64, top-8, few tokens: most experts empty (row table)
     ((128, 128, 4, 2, 128), 100),  # alignment 128: most packed rows are padding
+    ((128, 256, 8, 2), 2048),      # H=128: the down GEMM's 128-column halves past its last column
 ])
 def test_block_edge_configurations(cfg, tokens):
     _check_block(MoEConfig(*cfg), tokens, seed=tokens)

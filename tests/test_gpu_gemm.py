@@ -145,6 +145,39 @@ def test_schedule_does_not_change_results(ext, counts, alignment, n, k, swiglu, 
     assert rel_l2(got[:used], ref) < 3e-3
 
 
+# counts, alignment, n, grid: plans whose split tiles have 128- or 64-column pieces
+# starting at or past the last output column (N < 256, or a last column tile of
+# 64-192 columns); such a piece has no work and its weight rows would start past
+# the expert's (a wrapped buffer range once read past the weights).
+EDGE_PIECE_CASES = [
+    ([169], 1, 64, 8),
+    ([520, 20], 8, 192, 8),
+    ([1000, 20, 300], 8, 320, 24),
+    ([300, 420, 520, 700, 1034, 100], 8, 128, 24),
+    ([300, 420, 520, 700, 1034, 100], 8, 64, 0),
+]
+
+
+@pytest.mark.parametrize("counts,alignment,n,grid", EDGE_PIECE_CASES)
+def test_column_pieces_past_the_last_column(ext, counts, alignment, n, grid):
+    experts, k = len(counts), 256
+    a, offsets, rows = _inputs(counts, alignment, k, seed=n + grid)
+    g = torch.Generator(device="cuda").manual_seed(7 * n + grid)
+    b = (torch.randn(experts, n, k, device="cuda", generator=g) / k**0.5).bfloat16()
+    c = torch.full((rows, n), 7.0, device="cuda").bfloat16()
+    try:
+        ext.set_gemm_workgroups(grid)
+        ext.grouped_gemm_out(a, b, offsets, c)
+        torch.cuda.synchronize()
+    finally:
+        ext.set_gemm_workgroups(0)
+    used = int(to_np(offsets)[-1])
+    got = to_np(c)
+    mfma = oracle.grouped_gemm(to_np(a), to_np(b), to_np(offsets), order="mfma")
+    assert_near_bit_exact(got[:used], oracle.bf16_round(mfma)[:used])
+    assert np.all(got[used:] == 7.0), "rows past offsets[E] must not be written"
+
+
 # rows of A, ascending offsets as given (past the rows, negative), the same clamped to [0, rows]
 CLAMP_CASES = [
     (600, [0, 100, 2_000_000_000, 2_147_483_000], [0, 100, 600, 600]),
