@@ -84,7 +84,8 @@ def _check_block(cfg, tokens, pattern="balanced", seed=0, bias=None, large_i=Fal
     logits = oracle.router_logits(xf, router_w)
     ids_ref, w_ref, _ = oracle.topk_route(logits, bias_np, cfg.topk)
     safe = route_margin(logits, bias_np, cfg.topk) > 1e-4
-    assert safe.mean() > 0.99 or tokens < 20
+    # Near-ties are rare: at most 1% of the tokens (or one) are left out.
+    assert (~safe).sum() <= max(1, 0.01 * tokens) or tokens < 20
     np.testing.assert_array_equal(ids[safe], ids_ref[safe])
     np.testing.assert_allclose(w[safe], w_ref[safe], rtol=0, atol=2e-5)
     # Dispatch, bit-exact.
