@@ -8,6 +8,7 @@ inverse and every packed row inside the used spans. The same holds for replays
 of a graph that captured the entry point.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -63,6 +64,33 @@ def test_noalloc_dispatch_equals_workspace_dispatch(calls):
             assert torch.equal(got[name], getattr(ws, name)), (name, tokens)
         used = int(ws.offsets[-1])
         assert (raw_bits(got["packed"])[:used] == raw_bits(ws.packed)[:used]).all(), tokens
+
+
+def test_random_noalloc_dispatches_in_a_row():
+    """Thirty calls drawn from a fixed seed (fp16/fp32/bf16, any hidden size, 1-64
+    experts, top-1 to top-8, alignment 1-128, 1-8000 tokens), one after the other,
+    so each starts from the previous call's counters in the static array."""
+    lib = _lib.load_library()
+    rng = np.random.default_rng(61)
+    for case in range(30):
+        dtype = (torch.float16, torch.float32, torch.bfloat16)[int(rng.integers(0, 3))]
+        experts = int(rng.integers(1, 65))
+        topk = int(rng.integers(1, min(8, experts) + 1))
+        tokens = int(np.exp(rng.uniform(0, np.log(8000))))
+        hidden = int(rng.integers(1, 1500)) if rng.random() < 0.4 else 8 * int(rng.integers(1, 256))
+        while tokens * topk * hidden > 4e7:
+            tokens = max(1, tokens // 2)
+        alignment = int(rng.choice([1, 3, 8, 16, 128]))
+        print(f"case {case}: T={tokens} H={hidden} E={experts} K={topk} a={alignment} {dtype}", flush=True)
+        x, ids32, _, _ = make_transport_case(tokens, hidden, experts, topk, dtype, seed=200 + case)
+        ws = CudaWorkspace(tokens, hidden, experts, topk, dtype, alignment=alignment)
+        ws.dispatch(x, ids32)
+        got = _noalloc_dispatch(lib, x, ids32, experts, alignment, ws.capacity_rows)
+        torch.cuda.synchronize()
+        for name in ("counts", "offsets", "slots", "inverse"):
+            assert torch.equal(got[name], getattr(ws, name)), (name, case)
+        used = int(ws.offsets[-1])
+        assert (raw_bits(got["packed"])[:used] == raw_bits(ws.packed)[:used]).all(), case
 
 
 def test_noalloc_dispatch_validates_like_dispatch():
