@@ -26,11 +26,11 @@ int launch_dispatch_ranked(const void*, int, const int32_t*, int32_t*, int32_t*,
 int launch_combine(const void*, int, const int32_t*, const float*, void*, int64_t, int64_t, int,
                    int64_t, hipStream_t);
 int launch_swiglu(const void*, int, const int32_t*, void*, int64_t, int64_t, hipStream_t);
-int launch_grouped_gemm(const uint16_t*, const uint16_t*, uint16_t*, const int32_t*, int64_t,
+int launch_grouped_gemm(const uint16_t*, const uint16_t*, int64_t, uint16_t*, const int32_t*, int64_t,
                         int64_t, int64_t, int, hipStream_t);
-int launch_gateup_swiglu(const uint16_t*, const uint16_t*, uint16_t*, const int32_t*, int64_t,
+int launch_gateup_swiglu(const uint16_t*, const uint16_t*, int64_t, uint16_t*, const int32_t*, int64_t,
                          int64_t, int64_t, int, hipStream_t);
-int launch_gateup_swiglu_gathered(const uint16_t*, const int32_t*, int64_t, const uint16_t*, uint16_t*,
+int launch_gateup_swiglu_gathered(const uint16_t*, const int32_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
                                   const int32_t*, int64_t, int64_t, int64_t, int, hipStream_t);
 int launch_dispatch_rows(const int32_t*, int32_t*, int32_t*, int32_t*, int32_t*, int32_t*, const int32_t*, int32_t*,
                          int64_t, int64_t, int, int, int, int64_t, hipStream_t);
@@ -390,21 +390,37 @@ int moe_swiglu(const void* projection, int dtype, const int32_t* valid_rows, voi
                          static_cast<hipStream_t>(stream));
 }
 
+// The weights' row stride: at least the row length, a multiple of 8 (rows
+// start 16-byte aligned), and with rows * stride within the kernels' 32-bit
+// buffer ranges (one expert's weights, and a 256-row tile).
+static int check_row_stride(int64_t stride, int64_t k, int64_t weight_rows) {
+    MOE_REQUIRE(stride >= k && stride % 8 == 0 && stride <= INT_MAX, MOE_ERR_UNSUPPORTED,
+                "weight row stride must be a multiple of 8 and at least the row length");
+    MOE_REQUIRE(256 * stride * 2 <= UINT32_MAX && weight_rows <= UINT32_MAX / (2 * stride), MOE_ERR_CAPACITY,
+                "one expert's weight matrix must be below 4 GiB");
+    return MOE_OK;
+}
+
 int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offsets, int64_t rows,
                      int64_t n, int64_t k, int64_t experts, void* stream) {
+    return moe_grouped_gemm_strided(a, b, k, c, offsets, rows, n, k, experts, stream);
+}
+
+int moe_grouped_gemm_strided(const void* a, const void* b, int64_t b_row_stride, void* c, const int32_t* offsets,
+                             int64_t rows, int64_t n, int64_t k, int64_t experts, void* stream) {
     MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
     MOE_REQUIRE(rows >= 0 && rows <= INT_MAX, MOE_ERR_CAPACITY, "rows exceed int32");
     MOE_REQUIRE(n > 0 && k > 0 && n % 8 == 0 && k % 8 == 0, MOE_ERR_UNSUPPORTED,
                 "grouped GEMM dimensions must be positive multiples of 8");
     // The kernels bound each expert's weights and row tile with 32-bit buffer ranges.
-    MOE_REQUIRE(n <= INT_MAX && k <= INT_MAX && n * k * 2 <= UINT32_MAX && 256 * k * 2 <= UINT32_MAX,
-                MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
+    MOE_REQUIRE(n <= INT_MAX && k <= INT_MAX, MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
+    if (int status = check_row_stride(b_row_stride, k, n); status != MOE_OK) return status;
     if (rows == 0) return MOE_OK;
     MOE_REQUIRE(a && b && c && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
     // Operands are read with 16-byte buffer loads and results stored 8 bytes at a time.
     MOE_REQUIRE(aligned_to(a, 16) && aligned_to(b, 16) && aligned_to(c, 16) && aligned_to(offsets, 4),
                 MOE_ERR_INVALID_ARGUMENT, "a, b and c must be 16-byte aligned (offsets 4-byte)");
-    return launch_grouped_gemm(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+    return launch_grouped_gemm(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), b_row_stride,
                                static_cast<uint16_t*>(c), offsets, rows, n, k, (int)experts,
                                static_cast<hipStream_t>(stream));
 }
@@ -412,19 +428,26 @@ int moe_grouped_gemm(const void* a, const void* b, void* c, const int32_t* offse
 int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
                               const int32_t* offsets, int64_t rows, int64_t hidden,
                               int64_t intermediate, int64_t experts, void* stream) {
+    return moe_grouped_gateup_swiglu_strided(a, gate_up, hidden, act, offsets, rows, hidden, intermediate, experts,
+                                             stream);
+}
+
+int moe_grouped_gateup_swiglu_strided(const void* a, const void* gate_up, int64_t gate_up_row_stride, void* act,
+                                      const int32_t* offsets, int64_t rows, int64_t hidden, int64_t intermediate,
+                                      int64_t experts, void* stream) {
     MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
     MOE_REQUIRE(rows >= 0 && rows <= INT_MAX, MOE_ERR_CAPACITY, "rows exceed int32");
     MOE_REQUIRE(hidden > 0 && intermediate > 0 && hidden % 8 == 0 && intermediate % 8 == 0,
                 MOE_ERR_UNSUPPORTED, "grouped GEMM dimensions must be positive multiples of 8");
-    MOE_REQUIRE(hidden <= INT_MAX && intermediate <= INT_MAX && 2 * intermediate * hidden * 2 <= UINT32_MAX &&
-                    256 * hidden * 2 <= UINT32_MAX,
-                MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
+    MOE_REQUIRE(hidden <= INT_MAX && intermediate <= INT_MAX, MOE_ERR_CAPACITY,
+                "one expert's weight matrix must be below 4 GiB");
+    if (int status = check_row_stride(gate_up_row_stride, hidden, 2 * intermediate); status != MOE_OK) return status;
     if (rows == 0) return MOE_OK;
     MOE_REQUIRE(a && gate_up && act && offsets, MOE_ERR_INVALID_ARGUMENT, "null pointer");
     MOE_REQUIRE(aligned_to(a, 16) && aligned_to(gate_up, 16) && aligned_to(act, 16) && aligned_to(offsets, 4),
                 MOE_ERR_INVALID_ARGUMENT, "a, gate_up and act must be 16-byte aligned (offsets 4-byte)");
-    return launch_gateup_swiglu(static_cast<const uint16_t*>(a),
-                                static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(act),
+    return launch_gateup_swiglu(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(gate_up),
+                                gate_up_row_stride, static_cast<uint16_t*>(act),
                                 offsets, rows, hidden, intermediate, (int)experts,
                                 static_cast<hipStream_t>(stream));
 }
@@ -432,14 +455,22 @@ int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
 int moe_grouped_gateup_swiglu_gathered(const void* x, const int32_t* row_src, int64_t x_rows, const void* gate_up,
                                        void* act, const int32_t* offsets, int64_t rows, int64_t hidden,
                                        int64_t intermediate, int64_t experts, void* stream) {
+    return moe_grouped_gateup_swiglu_gathered_strided(x, row_src, x_rows, gate_up, hidden, act, offsets, rows, hidden,
+                                                      intermediate, experts, stream);
+}
+
+int moe_grouped_gateup_swiglu_gathered_strided(const void* x, const int32_t* row_src, int64_t x_rows,
+                                               const void* gate_up, int64_t gate_up_row_stride, void* act,
+                                               const int32_t* offsets, int64_t rows, int64_t hidden,
+                                               int64_t intermediate, int64_t experts, void* stream) {
     MOE_REQUIRE(experts >= 1 && experts <= kMaxExperts, MOE_ERR_UNSUPPORTED, "supports 1..64 experts");
     MOE_REQUIRE(rows >= 0 && rows <= INT_MAX && x_rows >= 0 && x_rows <= INT_MAX, MOE_ERR_CAPACITY,
                 "rows exceed int32");
     MOE_REQUIRE(hidden > 0 && intermediate > 0 && hidden % 64 == 0 && intermediate % 8 == 0, MOE_ERR_UNSUPPORTED,
                 "gathered gate/up needs hidden a positive multiple of 64 and intermediate of 8");
-    MOE_REQUIRE(hidden <= INT_MAX && intermediate <= INT_MAX && 2 * intermediate * hidden * 2 <= UINT32_MAX &&
-                    256 * hidden * 2 <= UINT32_MAX,
-                MOE_ERR_CAPACITY, "one expert's weight matrix must be below 4 GiB");
+    MOE_REQUIRE(hidden <= INT_MAX && intermediate <= INT_MAX, MOE_ERR_CAPACITY,
+                "one expert's weight matrix must be below 4 GiB");
+    if (int status = check_row_stride(gate_up_row_stride, hidden, 2 * intermediate); status != MOE_OK) return status;
     // x is one buffer of 32-bit offsets, with 2 GiB and up left for the out-of-range marker.
     MOE_REQUIRE(x_rows * hidden * 2 < (int64_t{1} << 31), MOE_ERR_CAPACITY, "x must be below 2 GiB");
     if (rows == 0) return MOE_OK;
@@ -448,7 +479,8 @@ int moe_grouped_gateup_swiglu_gathered(const void* x, const int32_t* row_src, in
                     aligned_to(row_src, 4),
                 MOE_ERR_INVALID_ARGUMENT, "x, gate_up and act must be 16-byte aligned (index buffers 4-byte)");
     return launch_gateup_swiglu_gathered(static_cast<const uint16_t*>(x), row_src, x_rows,
-                                         static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(act), offsets,
+                                         static_cast<const uint16_t*>(gate_up), gate_up_row_stride,
+                                         static_cast<uint16_t*>(act), offsets,
                                          rows, hidden, intermediate, (int)experts, static_cast<hipStream_t>(stream));
 }
 

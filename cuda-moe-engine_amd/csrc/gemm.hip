@@ -44,10 +44,11 @@ constexpr int kBK = 64;  // k-step: one 128-byte LDS row
 
 struct GemmParams {
     const uint16_t* a;        // [R, K], or with a_rows the [a_src_rows, K] rows they index
-    const uint16_t* b;        // [E, NB, K]  (NB = N, or 2I for gate/up)
+    const uint16_t* b;        // [E, NB, ldb]: K values per row, rows ldb apart (NB = N, or 2I for gate/up)
     uint16_t* c;              // [R, ldc]
     const int32_t* offsets;   // [E + 1]
     int64_t k;                // reduction length (H or I)
+    int64_t ldb;              // elements from one row of B to the next (>= k)
     int64_t nb;               // rows of one expert's B
     int64_t n_out;            // output columns (N, or I for gate/up)
     int64_t ldc;
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
     int b_dst[B_LOADS];
     bool b_ok[B_LOADS];
     int b_kc[B_LOADS];
-    const uint16_t* b_expert = p.b + static_cast<int64_t>(expert) * p.nb * p.k;
+    const uint16_t* b_expert = p.b + static_cast<int64_t>(expert) * p.nb * p.ldb;
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
         const int chunk = tid + i * kGemmThreads;
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmParams p
             brow = col;
         }
         b_ok[i] = ok;
-        b_src[i] = b_expert + (ok ? brow : 0) * p.k + c * 8;
+        b_src[i] = b_expert + (ok ? brow : 0) * p.ldb + c * 8;
         b_dst[i] = swz(r, c);
         b_kc[i] = c * 8;
     }
@@ -417,8 +418,8 @@ struct RingOps {
         // zero rows costs the gate/up persistent kernel 28 VGPRs, and at 4096
         // tokens, H=4096, I=14336, 8 experts, top-2, 14% of gate/up's time and
         // 10% of down's.
-        r.b = make_rsrc(p.b + (static_cast<int64_t>(expert) * p.nb + col0) * K,
-                        static_cast<uint32_t>((p.nb - col0) * K * 2));
+        r.b = make_rsrc(p.b + (static_cast<int64_t>(expert) * p.nb + col0) * p.ldb,
+                        static_cast<uint32_t>((p.nb - col0) * p.ldb * 2));
         if constexpr (GATHER) {
             r.a = make_rsrc(p.a, static_cast<uint32_t>(p.a_src_rows * K * 2));
             if (!offsets) return r;
@@ -458,7 +459,6 @@ struct RingOps {
     __device__ __forceinline__ RingOps(const GemmParams& p, char* lds_, const Rsrc& res) : lds(lds_) {
         const int lane = threadIdx.x & 63;
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        const int64_t K = p.k;
         rsrc_a = res.a;
         rsrc_b = res.b;
         const int lrow = lane >> 3;
@@ -479,7 +479,7 @@ struct RingOps {
             } else {
                 brow = r;
             }
-            b_off[i] = static_cast<uint32_t>((brow * K + (pchunk ^ ring_key(r)) * 8) * 2);
+            b_off[i] = static_cast<uint32_t>((brow * p.ldb + (pchunk ^ ring_key(r)) * 8) * 2);
         }
     }
     // Load l of stage kt into ring slot st, of A and of B (of this tile, or of
@@ -1512,7 +1512,7 @@ static int launch_gemm_t(GemmParams p, int64_t rows, hipStream_t stream) {
     return check_launch("grouped_gemm_kernel");
 }
 
-int launch_grouped_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, const int32_t* offsets,
+int launch_grouped_gemm(const uint16_t* a, const uint16_t* b, int64_t ldb, uint16_t* c, const int32_t* offsets,
                         int64_t rows, int64_t n, int64_t k, int experts, hipStream_t stream) {
     GemmParams p{};
     p.rows = rows;
@@ -1521,6 +1521,7 @@ int launch_grouped_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, const
     p.c = c;
     p.offsets = offsets;
     p.k = k;
+    p.ldb = ldb;
     p.nb = n;
     p.n_out = n;
     p.ldc = n;
@@ -1528,7 +1529,7 @@ int launch_grouped_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, const
     return launch_gemm_t<256, 256, 2, 2, false>(p, rows, stream);
 }
 
-int launch_gateup_swiglu(const uint16_t* a, const uint16_t* gate_up, uint16_t* act,
+int launch_gateup_swiglu(const uint16_t* a, const uint16_t* gate_up, int64_t ldb, uint16_t* act,
                          const int32_t* offsets, int64_t rows, int64_t hidden,
                          int64_t intermediate, int experts, hipStream_t stream) {
     GemmParams p{};
@@ -1538,6 +1539,7 @@ int launch_gateup_swiglu(const uint16_t* a, const uint16_t* gate_up, uint16_t* a
     p.c = act;
     p.offsets = offsets;
     p.k = hidden;
+    p.ldb = ldb;
     p.nb = 2 * intermediate;
     p.n_out = intermediate;
     p.ldc = intermediate;
@@ -1549,7 +1551,7 @@ int launch_gateup_swiglu(const uint16_t* a, const uint16_t* gate_up, uint16_t* a
 // negative): the dispatch's row table instead of its packed copy. Needs the
 // ring kernels (hidden a multiple of 64; the ABI checks it).
 int launch_gateup_swiglu_gathered(const uint16_t* x, const int32_t* a_rows, int64_t x_rows, const uint16_t* gate_up,
-                                  uint16_t* act, const int32_t* offsets, int64_t rows, int64_t hidden,
+                                  int64_t ldb, uint16_t* act, const int32_t* offsets, int64_t rows, int64_t hidden,
                                   int64_t intermediate, int experts, hipStream_t stream) {
     GemmParams p{};
     p.rows = rows;
@@ -1560,6 +1562,7 @@ int launch_gateup_swiglu_gathered(const uint16_t* x, const int32_t* a_rows, int6
     p.c = act;
     p.offsets = offsets;
     p.k = hidden;
+    p.ldb = ldb;
     p.nb = 2 * intermediate;
     p.n_out = intermediate;
     p.ldc = intermediate;

@@ -38,6 +38,34 @@ def _check_gpu_tensor(tensor, anchor, name):
     _check(tensor.device == anchor.device, f"{name}: device mismatch")
 
 
+def weight_row_stride(weight):
+    """Elements from one row of a ``[E, N, K]`` weight tensor to the next when its
+    rows are contiguous and evenly spaced (a contiguous tensor: K; a ``[:, :, :K]``
+    view of row-padded storage: the padded length), else None."""
+    if weight.dim() != 3:
+        return None
+    experts, rows, k = weight.shape
+    if k > 1 and weight.stride(2) != 1:
+        return None
+    # Row j of expert e sits at element (e * rows + j) * stride.
+    stride = weight.stride(1) if rows > 1 else (weight.stride(0) if experts > 1 else k)
+    if stride < k or (experts > 1 and weight.stride(0) != rows * stride):
+        return None
+    return stride
+
+
+def _check_weight(weight, anchor, name):
+    """A GPU weight tensor on x's device whose rows the GEMM kernels can read: contiguous,
+    or rows padded to a multiple of 8 elements (16-byte aligned rows)."""
+    _check(isinstance(weight, torch.Tensor), f"{name} must be a tensor")
+    _check(weight.is_cuda, f"{name}: all tensors must be GPU tensors")
+    _check(weight.device == anchor.device, f"{name}: device mismatch")
+    stride = weight_row_stride(weight)
+    _check(stride is not None and stride % 8 == 0,
+           f"{name}: weights must be contiguous, or [E, N, K] rows padded to a multiple of 8 elements")
+    return stride
+
+
 def current_stream_handle(device_index):
     """The current torch stream's HIP handle on a device (torch's raw accessor when it has one)."""
     raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -260,18 +288,18 @@ class HipExtension:
 
     def grouped_gemm_out(self, x, weight, offsets, output):
         """``output[r] = x[r] @ weight[e]^T`` for rows of expert e (bf16, fp32 accumulate)."""
-        self._check_gemm(x, weight, offsets, output, weight.shape[1])
-        status = self.lib.moe_grouped_gemm(
-            _ptr(x), _ptr(weight), _ptr(output), _ptr(offsets), x.shape[0], weight.shape[1],
+        stride = self._check_gemm(x, weight, offsets, output, weight.shape[1])
+        status = self.lib.moe_grouped_gemm_strided(
+            _ptr(x), _ptr(weight), stride, _ptr(output), _ptr(offsets), x.shape[0], weight.shape[1],
             x.shape[1], weight.shape[0], _stream(x.device))
         self.lib.check(status, "grouped_gemm_out")
 
     def gateup_swiglu_out(self, x, gate_up, offsets, output):
         """Gate/up grouped GEMM with the SwiGLU epilogue fused; output is ``[R, I]``."""
         _check(gate_up.dim() == 3 and gate_up.shape[1] % 2 == 0, "expected gate_up[E,2I,H]")
-        self._check_gemm(x, gate_up, offsets, output, gate_up.shape[1] // 2)
-        status = self.lib.moe_grouped_gateup_swiglu(
-            _ptr(x), _ptr(gate_up), _ptr(output), _ptr(offsets), x.shape[0], x.shape[1],
+        stride = self._check_gemm(x, gate_up, offsets, output, gate_up.shape[1] // 2)
+        status = self.lib.moe_grouped_gateup_swiglu_strided(
+            _ptr(x), _ptr(gate_up), stride, _ptr(output), _ptr(offsets), x.shape[0], x.shape[1],
             gate_up.shape[1] // 2, gate_up.shape[0], _stream(x.device))
         self.lib.check(status, "gateup_swiglu_out")
 
@@ -285,14 +313,15 @@ class HipExtension:
         _check(row_src.dtype == torch.int32 and row_src.dim() == 1, "expected int32 row_src[R]")
         rows = row_src.numel()
         _check(x.shape[1] % 64 == 0, "gathered gate/up needs hidden a multiple of 64")
-        for name, t in (("gate_up", gate_up), ("offsets", offsets), ("output", output)):
+        stride = _check_weight(gate_up, x, "gate_up")
+        for name, t in (("offsets", offsets), ("output", output)):
             _check_gpu_tensor(t, x, name)
         _check(gate_up.dtype == torch.bfloat16 and gate_up.shape[2] == x.shape[1], "expected BF16 gate_up matching x")
         _check(offsets.dtype == torch.int32 and offsets.numel() == gate_up.shape[0] + 1, "expected int32 offsets[E+1]")
         _check(output.shape == (rows, gate_up.shape[1] // 2) and output.dtype == torch.bfloat16,
                "incorrect grouped-GEMM output buffer")
-        status = self.lib.moe_grouped_gateup_swiglu_gathered(
-            _ptr(x), _ptr(row_src), x.shape[0], _ptr(gate_up), _ptr(output), _ptr(offsets), rows, x.shape[1],
+        status = self.lib.moe_grouped_gateup_swiglu_gathered_strided(
+            _ptr(x), _ptr(row_src), x.shape[0], _ptr(gate_up), stride, _ptr(output), _ptr(offsets), rows, x.shape[1],
             gate_up.shape[1] // 2, gate_up.shape[0], _stream(x.device))
         self.lib.check(status, "gateup_swiglu_gathered_out")
 
@@ -305,15 +334,18 @@ class HipExtension:
     def _check_gemm(x, weight, offsets, output, out_cols):
         _check(x.is_cuda and x.is_contiguous() and x.dim() == 2 and x.dtype == torch.bfloat16,
                "expected contiguous BF16 GPU x[R,K]")
-        for name, t in (("weight", weight), ("offsets", offsets), ("output", output)):
+        _check(isinstance(weight, torch.Tensor) and weight.dim() == 3, "expected BF16 weight[E,N,K] matching x")
+        stride = _check_weight(weight, x, "weight")
+        for name, t in (("offsets", offsets), ("output", output)):
             _check_gpu_tensor(t, x, name)
-        _check(weight.dim() == 3 and weight.dtype == torch.bfloat16 and weight.shape[2] == x.shape[1],
+        _check(weight.dtype == torch.bfloat16 and weight.shape[2] == x.shape[1],
                "expected BF16 weight[E,N,K] matching x")
         _check(offsets.dtype == torch.int32 and offsets.numel() == weight.shape[0] + 1,
                "expected int32 offsets[E+1]")
         _check(output.shape == (x.shape[0], out_cols) and output.dtype == torch.bfloat16,
                "incorrect grouped-GEMM output buffer")
         _check(x.shape[1] % 8 == 0 and out_cols % 8 == 0, "grouped GEMM dimensions must be multiples of 8")
+        return stride
 
 
 @lru_cache(maxsize=1)

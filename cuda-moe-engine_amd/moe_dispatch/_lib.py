@@ -13,7 +13,7 @@ from functools import lru_cache
 from pathlib import Path
 
 LIBRARY_NAME = "libmoe_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -55,6 +55,11 @@ _SIGNATURES = {
     "moe_grouped_gateup_swiglu": (_int, [_c_void_p] * 4 + [_i64] * 4 + [_c_void_p]),
     "moe_grouped_gateup_swiglu_gathered": (_int, [_c_void_p, _c_void_p, _i64] + [_c_void_p] * 3 + [_i64] * 4
                                            + [_c_void_p]),
+    "moe_grouped_gemm_strided": (_int, [_c_void_p, _c_void_p, _i64] + [_c_void_p] * 2 + [_i64] * 4 + [_c_void_p]),
+    "moe_grouped_gateup_swiglu_strided": (_int, [_c_void_p, _c_void_p, _i64] + [_c_void_p] * 2 + [_i64] * 4
+                                          + [_c_void_p]),
+    "moe_grouped_gateup_swiglu_gathered_strided": (_int, [_c_void_p, _c_void_p, _i64, _c_void_p, _i64]
+                                                   + [_c_void_p] * 2 + [_i64] * 4 + [_c_void_p]),
     "moe_set_gemm_workgroups": (_int, [_i64]),
 }
 

@@ -22,6 +22,7 @@
  *   packed       [R, H]       rows grouped by expert; span e = [offsets[e], offsets[e+1])
  *   gate_up      [E, 2I, H]   bf16; rows 0..I-1 gate, I..2I-1 up
  *   down         [E, H, I]    bf16
+ *   (the *_strided GEMM entry points also take weight rows further apart)
  *
  * Slot order is canonical (deterministic): within an expert, assignments
  * appear in increasing flat index p. No global atomics are used.
@@ -35,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 7
+#define MOE_ABI_VERSION 8
 
 typedef enum {
     MOE_DTYPE_F32 = 0,
@@ -284,6 +285,30 @@ int moe_grouped_gateup_swiglu(const void* a, const void* gate_up, void* act,
 int moe_grouped_gateup_swiglu_gathered(const void* x, const int32_t* row_src, int64_t x_rows, const void* gate_up,
                                        void* act, const int32_t* offsets, int64_t rows, int64_t hidden,
                                        int64_t intermediate, int64_t experts, void* stream);
+
+/*
+ * The three GEMMs above with the weights' rows a given number of elements
+ * apart: row j of expert e's weights starts at element (e * NB + j) * stride
+ * (NB = n, or 2 * intermediate for gate/up), and its first k (or hidden)
+ * elements are read. With stride equal to the row length they are the calls
+ * above (which call these). Every output is the same MFMA chain, so results
+ * equal those on a contiguous copy of the weights bit for bit. For weights
+ * stored with padded rows: rows a power of two bytes apart (gate/up at
+ * H = 4096) are read in lockstep by the weight-streaming kernels, and 64
+ * elements of padding per row make the gate/up GEMM at 1 and 16 tokens,
+ * H = 4096, 10-11% faster. Requires stride >= the row length, stride % 8
+ * == 0, and one expert's rows * stride * 2 bytes below 4 GiB. No counterpart
+ * in the reference (its weights are contiguous tensors).
+ */
+int moe_grouped_gemm_strided(const void* a, const void* b, int64_t b_row_stride, void* c, const int32_t* offsets,
+                             int64_t rows, int64_t n, int64_t k, int64_t experts, void* stream);
+int moe_grouped_gateup_swiglu_strided(const void* a, const void* gate_up, int64_t gate_up_row_stride, void* act,
+                                      const int32_t* offsets, int64_t rows, int64_t hidden, int64_t intermediate,
+                                      int64_t experts, void* stream);
+int moe_grouped_gateup_swiglu_gathered_strided(const void* x, const int32_t* row_src, int64_t x_rows,
+                                               const void* gate_up, int64_t gate_up_row_stride, void* act,
+                                               const int32_t* offsets, int64_t rows, int64_t hidden,
+                                               int64_t intermediate, int64_t experts, void* stream);
 
 /*
  * Upper bound on the workgroups of the persistent grouped GEMM (both

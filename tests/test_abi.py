@@ -156,6 +156,28 @@ def test_misaligned_pointers_are_rejected_without_launching():
     assert lib.moe_swiglu(A + 1, 2, A, A, 4, 64, None) == 1
 
 
+def test_strided_gemm_arguments_are_checked_without_launching():
+    """The row stride of the _strided entry points: at least the row length, a
+    multiple of 8, and one expert's rows * stride within 4 GiB."""
+    lib = _lib.load_library()
+    A = 1 << 20  # 16-byte aligned stand-in addresses (never dereferenced)
+    # a, b, stride, c, offsets, rows, n, k, E
+    assert lib.moe_grouped_gemm_strided(A, A, 56, A, A, 16, 64, 64, 1, None) == 2
+    assert b"row stride" in lib.moe_last_error()
+    assert lib.moe_grouped_gemm_strided(A, A, 68, A, A, 16, 64, 64, 1, None) == 2
+    assert lib.moe_grouped_gemm_strided(A, A, 1 << 22, A, A, 16, 1024, 64, 1, None) == 3
+    assert b"4 GiB" in lib.moe_last_error()
+    assert lib.moe_grouped_gemm_strided(A, A + 8, 72, A, A, 16, 64, 64, 1, None) == 1
+    assert lib.moe_grouped_gemm_strided(A, A, 72, A, A, 0, 64, 64, 1, None) == 0  # no rows
+    # a, gate_up, stride, act, offsets, rows, H, I, E
+    assert lib.moe_grouped_gateup_swiglu_strided(A, A, 60, A, A, 16, 64, 64, 1, None) == 2
+    assert lib.moe_grouped_gateup_swiglu_strided(A, A, 1 << 16, A, A, 16, 64, 1 << 15, 1, None) == 3
+    assert lib.moe_grouped_gateup_swiglu_strided(A, A, 128, A, A, 0, 64, 64, 1, None) == 0
+    # x, row_src, x_rows, gate_up, stride, act, offsets, rows, H, I, E
+    assert lib.moe_grouped_gateup_swiglu_gathered_strided(A, A, 16, A, 63, A, A, 16, 64, 64, 1, None) == 2
+    assert lib.moe_grouped_gateup_swiglu_gathered_strided(A, A, 16, A, 128, A, A, 0, 64, 64, 1, None) == 0
+
+
 def test_error_surfaces_as_runtime_error():
     lib = _lib.load_library()
     with pytest.raises(_lib.MoeHipError, match="1..64"):

@@ -79,3 +79,29 @@ def test_extension_refuses_without_gpu():
 
     with pytest.raises(RuntimeError, match="GPU"):
         get_extension()
+
+
+def test_weight_row_stride_of_each_layout():
+    from moe_dispatch._extension import weight_row_stride
+
+    w = torch.zeros(4, 6, 16)
+    assert weight_row_stride(w) == 16
+    assert weight_row_stride(torch.zeros(4, 6, 24)[:, :, :16]) == 24
+    assert weight_row_stride(torch.zeros(3, 1, 24)[:, :, :16]) == 24  # one row per expert
+    assert weight_row_stride(torch.zeros(1, 1, 16)) == 16
+    assert weight_row_stride(w.transpose(1, 2)) is None  # columns contiguous, not rows
+    assert weight_row_stride(w[:, ::2]) == 32  # every other row: evenly spaced
+    assert weight_row_stride(torch.zeros(4, 12, 16)[::2, :6]) is None  # experts not rows * stride apart
+    assert weight_row_stride(torch.zeros(6, 16)) is None
+
+
+def test_fused_block_pads_power_of_two_gate_up_rows():
+    from moe_dispatch.layer import GATE_UP_ROW_PADDING, padded_gate_up
+
+    for hidden, padded in ((4096, True), (8192, True), (2048, False), (6144, False), (512, False)):
+        w = torch.randn(2, 8, hidden).bfloat16()
+        p = padded_gate_up(w)
+        assert torch.equal(p, w)
+        assert p.stride(1) == (hidden + GATE_UP_ROW_PADDING if padded else hidden), hidden
+    # fp32 rows of 2048 elements are 8 KiB: padded too.
+    assert padded_gate_up(torch.zeros(1, 2, 2048)).stride(1) == 2048 + GATE_UP_ROW_PADDING

@@ -28,7 +28,7 @@ import numpy as np
 import pytest
 import torch
 
-from moe_dispatch.layer import MoEBlock, MoEConfig
+from moe_dispatch.layer import GATE_UP_ROW_PADDING, MoEBlock, MoEConfig
 from oracle import moe_oracle as oracle
 from tests._helpers import LazyExpertWeights, assert_near_bit_exact, gpu, rel_l2, route_margin, to_np
 
@@ -283,6 +283,27 @@ def test_repeat_calls_follow_weight_changes_and_streams():
         out = block(x).clone()
     torch.cuda.current_stream().wait_stream(side)
     assert torch.equal(out, twin(x))
+
+
+@pytest.mark.parametrize("cfg", [MoEConfig(4096, 256, 8, 2), MoEConfig(4096, 192, 16, 6)])
+def test_padded_gate_up_rows_equal_contiguous_weights(cfg):
+    """H = 4096: the fused block keeps its gate/up rows padded (8 KiB rows). Its
+    forward equals a twin's whose gate/up weights are a contiguous copy, bit for
+    bit, on the weight-streaming and persistent paths (and at top-6 the gathered
+    gate/up GEMM); in-place updates through the padded view reach the kernels."""
+    block = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=3)
+    assert block.gate_up_weight.stride(1) == cfg.hidden + GATE_UP_ROW_PADDING
+    twin = MoEBlock(cfg, device="cuda", implementation="cuda_fused", seed=3)
+    twin.gate_up_weight = block.gate_up_weight.contiguous()
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    for tokens in (1, 16, 700):
+        x = torch.randn(tokens, cfg.hidden, device="cuda", generator=gen).bfloat16()
+        assert torch.equal(block(x).clone(), twin(x)), tokens
+    new = (torch.randn(block.gate_up_weight.shape, device="cuda", generator=gen) / 45).bfloat16()
+    block.gate_up_weight.copy_(new)
+    twin.gate_up_weight.copy_(new)
+    x = torch.randn(300, cfg.hidden, device="cuda", generator=gen).bfloat16()
+    assert torch.equal(block(x).clone(), twin(x))
 
 
 def test_empty_batch():

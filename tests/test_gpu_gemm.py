@@ -246,3 +246,64 @@ def test_gateup_swiglu_matches_unfused_pipeline(ext, counts, alignment, hidden, 
     unfused = torch.empty_like(act)
     ext.swiglu_out(projection, offsets[-1:], unfused)
     assert_near_bit_exact(got[:used], to_np(unfused)[:used], max_fraction=1e-4, max_steps=1.0)
+
+
+STRIDED_CASES = [
+    # counts per expert, alignment, n (intermediate for gate/up), k (hidden), padding per row
+    ([2, 2], 1, 1024, 4096, 64),                 # weight-streaming kernel, 64-row instance
+    ([60, 40, 20], 8, 512, 2048, 64),            # weight-streaming kernel, 128-row instance
+    ([700, 3, 0, 260, 1100], 8, 384, 1024, 64),  # persistent kernel: full, short and split tiles
+    ([300, 420, 520, 700, 1034, 100], 8, 128, 512, 8),
+    ([1500, 100, 3, 0], 8, 256, 200, 8),         # generic kernel (K % 64 != 0)
+]
+
+
+def _row_padded(w, pad):
+    """w as a [:, :, :K] view of storage with `pad` NaN elements after each row."""
+    e, n, k = w.shape
+    storage = torch.full((e, n, k + pad), float("nan"), device=w.device, dtype=w.dtype)
+    storage[:, :, :k] = w
+    view = storage[:, :, :k]
+    assert not view.is_contiguous() and view.stride(1) == k + pad
+    return view
+
+
+@pytest.mark.parametrize("counts,alignment,n,k,pad", STRIDED_CASES)
+def test_row_padded_weights_equal_contiguous(ext, counts, alignment, n, k, pad):
+    """Weights read through a row stride (the _strided entry points, through the
+    extension's view handling) give the contiguous weights' outputs bit for bit:
+    the plain GEMM, the gate/up GEMM with the SwiGLU epilogue, and the gathered
+    gate/up GEMM. The padding holds NaN, so a read of it would show."""
+    experts = len(counts)
+    a, offsets, rows = _inputs(counts, alignment, k, seed=k + n + pad)
+    g = torch.Generator(device="cuda").manual_seed(7 * k + n)
+    w = (torch.randn(experts, n, k, device="cuda", generator=g) / k**0.5).bfloat16()
+    gu = (torch.randn(experts, 2 * n, k, device="cuda", generator=g) / k**0.5).bfloat16()
+    used = int(to_np(offsets)[-1])
+    plain = [torch.full((rows, n), 3.0, device="cuda").bfloat16() for _ in range(2)]
+    ext.grouped_gemm_out(a, w, offsets, plain[0])
+    ext.grouped_gemm_out(a, _row_padded(w, pad), offsets, plain[1])
+    act = [torch.full((rows, n), 3.0, device="cuda").bfloat16() for _ in range(2)]
+    ext.gateup_swiglu_out(a, gu, offsets, act[0])
+    ext.gateup_swiglu_out(a, _row_padded(gu, pad), offsets, act[1])
+    for got, ref in (plain[::-1], act[::-1]):
+        assert torch.equal(got, ref)
+        assert not torch.isnan(got[:used].float()).any()
+    if k % 64 == 0:
+        row_src = torch.arange(rows, device="cuda", dtype=torch.int32)
+        gathered = [torch.full((rows, n), 3.0, device="cuda").bfloat16() for _ in range(2)]
+        ext.gateup_swiglu_gathered_out(a, row_src, gu, offsets, gathered[0])
+        ext.gateup_swiglu_gathered_out(a, row_src, _row_padded(gu, pad), offsets, gathered[1])
+        assert torch.equal(gathered[0], gathered[1])
+        assert torch.equal(gathered[0], act[0])
+
+
+def test_weights_of_other_layouts_are_refused(ext):
+    a, offsets, rows = _inputs([10, 20], 8, 64, seed=1)
+    out = torch.empty(rows, 64, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(2, 64, 64, device="cuda").bfloat16()
+    with pytest.raises(RuntimeError, match="contiguous, or"):
+        ext.grouped_gemm_out(a, w.transpose(1, 2), offsets, out)  # columns, not rows, contiguous
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        storage = torch.zeros(2, 64, 68, device="cuda").bfloat16()
+        ext.grouped_gemm_out(a, storage[:, :, :64], offsets, out)  # rows not 16-byte aligned
