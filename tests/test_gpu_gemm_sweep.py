@@ -10,7 +10,10 @@ bars as test_gpu_gemm.py:
   (plain GEMM, bf16 projection, standalone SwiGLU), the projection against the
   oracle;
 * the gathered gate/up GEMM (rows read from x through a row table with -1
-  entries) bit-exact against the packed one on the gathered rows.
+  entries) bit-exact against the packed one on the gathered rows;
+* every one of them again on the same weights stored with padded rows (a
+  [:, :, :K] view of storage with 8-1024 NaN elements after each row, read
+  through the row-stride entry points): bit-exact against contiguous weights.
 
 This sweep found the column pieces past the last output column
 (test_gpu_gemm.py::test_column_pieces_past_the_last_column).
@@ -61,7 +64,17 @@ def _cases(seed):
         yield case, experts, offsets, rows, k, n, grid, swiglu
 
 
-def _plain(ext, g, experts, offsets, rows, k, n):
+def _row_padded(w, case):
+    """w as a [:, :, :K] view of storage with NaN padding after each row (8 to 1024
+    elements, a multiple of 8, by case)."""
+    pad = (8, 64, 136, 1024)[case % 4]
+    e, n, k = w.shape
+    storage = torch.full((e, n, k + pad), float("nan"), device=w.device, dtype=w.dtype)
+    storage[:, :, :k] = w
+    return storage[:, :, :k]
+
+
+def _plain(ext, g, experts, offsets, rows, k, n, case):
     a = torch.randn(rows, k, device="cuda", generator=g).bfloat16()
     w = (torch.randn(experts, n, k, device="cuda", generator=g) / k**0.5).bfloat16()
     c = torch.full((rows, n), 7.0, device="cuda").bfloat16()
@@ -72,9 +85,12 @@ def _plain(ext, g, experts, offsets, rows, k, n):
     ref = oracle.bf16_round(oracle.grouped_gemm(to_np(a), to_np(w), offsets, order="mfma"))
     assert_near_bit_exact(got[:used], ref[:used])
     assert np.all(got[used:] == 7.0), "rows past offsets[E] must not be written"
+    padded = torch.full((rows, n), 7.0, device="cuda").bfloat16()
+    ext.grouped_gemm_out(a, _row_padded(w, case), torch.tensor(offsets, device="cuda"), padded)
+    assert torch.equal(padded, c), "row-padded weights differ from contiguous ones"
 
 
-def _gateup(ext, g, experts, offsets, rows, k, n):
+def _gateup(ext, g, experts, offsets, rows, k, n, case):
     inter = max(n // 2 // 8 * 8, 8)
     off = torch.tensor(offsets, device="cuda")
     used = int(offsets[-1])
@@ -103,6 +119,13 @@ def _gateup(ext, g, experts, offsets, rows, k, n):
     ext.gateup_swiglu_out(packed, w, off, act_p)
     torch.cuda.synchronize()
     assert torch.equal(act_g, act_p), "the gathered GEMM differs from the packed one on the same rows"
+    w_padded = _row_padded(w, case)
+    act_padded = torch.full((rows, inter), 3.0, device="cuda").bfloat16()
+    ext.gateup_swiglu_out(a, w_padded, off, act_padded)
+    assert torch.equal(act_padded, act), "row-padded weights differ from contiguous ones"
+    act_padded.fill_(3.0)
+    ext.gateup_swiglu_gathered_out(x, src, w_padded, off, act_padded)
+    assert torch.equal(act_padded, act_g), "row-padded weights differ from contiguous ones (gathered)"
 
 
 @pytest.mark.parametrize("seed", [1, 2, 3])
@@ -114,8 +137,8 @@ def test_random_grouped_gemms(ext, seed):
         try:
             ext.set_gemm_workgroups(grid)
             if swiglu:
-                _gateup(ext, g, experts, offsets, rows, k, n)
+                _gateup(ext, g, experts, offsets, rows, k, n, case)
             else:
-                _plain(ext, g, experts, offsets, rows, k, n)
+                _plain(ext, g, experts, offsets, rows, k, n, case)
         finally:
             ext.set_gemm_workgroups(0)
