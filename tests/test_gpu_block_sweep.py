@@ -5,6 +5,9 @@ routing), each checked stage by stage against the oracle as in
 test_gpu_block.py. Hand-picked configurations missed a block with hidden 128,
 whose down GEMM split its last column tile into pieces past the last column.
 
+A second set fixes H = 4096, where the fused block keeps its gate/up weight
+rows padded (8 KiB rows), with small intermediate sizes.
+
 Tokens start at 32: with one or a few tokens a single bf16 rounding flip can
 move the output past the 5e-4 relative-L2 bound against the exact-arithmetic
 token-major oracle (the kernel-order oracle's bound holds at any size).
@@ -43,3 +46,27 @@ def test_random_blocks(seed):
         print(f"seed {seed} case {case}: T={tokens} H={cfg.hidden} I={cfg.intermediate} E={cfg.experts} "
               f"K={cfg.topk} a={cfg.alignment} {pattern}", flush=True)
         _check_block(cfg, tokens, pattern, seed=100 * seed + case)
+
+
+def _padded_row_configs(seed, n):
+    """H = 4096 (gate/up rows of 8 KiB, which the fused block stores padded), small
+    intermediate sizes so that the CPU oracle stays fast, and token counts on both
+    the weight-streaming and the persistent paths."""
+    rng = np.random.default_rng(seed)
+    for case in range(n):
+        inter = 64 * int(rng.integers(1, 5))
+        experts = int(rng.choice([1, 2, 4, 8, 16, 32, 64]))
+        topk = int(rng.integers(1, min(8, experts) + 1))
+        alignment = int(rng.choice([8, 16, 64]))
+        tokens = int(np.exp(rng.uniform(np.log(32), np.log(1500))))
+        while tokens > 32 and tokens * topk * 4096 * inter > 4e8:
+            tokens = max(32, tokens // 2)
+        pattern = str(rng.choice(["balanced", "skewed"]))
+        yield case, MoEConfig(4096, inter, experts, topk, alignment), tokens, pattern
+
+
+def test_random_blocks_with_padded_gate_up_rows():
+    for case, cfg, tokens, pattern in _padded_row_configs(23, 8):
+        print(f"case {case}: T={tokens} H={cfg.hidden} I={cfg.intermediate} E={cfg.experts} K={cfg.topk} "
+              f"a={cfg.alignment} {pattern}", flush=True)
+        _check_block(cfg, tokens, pattern, seed=2300 + case)
