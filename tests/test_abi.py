@@ -34,6 +34,35 @@ def test_header_declares_the_binding_table():
     assert declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
 
 
+def _declarations():
+    """name -> (return kind, [parameter kinds]) from the header, kinds being
+    'p' (any pointer), 'i64' (int64_t) and 'i' (int)."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(r"([A-Za-z_][\w \*]*?)\b(moe_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        def kind(decl):
+            decl = decl.strip()
+            if "*" in decl:
+                return "p"
+            return "i64" if decl.startswith("int64_t") else "i"
+        ret = ret.split("\n")[-1].strip()
+        args = [] if params.strip() in ("", "void") else [kind(x) for x in params.split(",")]
+        out[name] = (kind(ret + " x"), args)
+    return out
+
+
+def test_binding_table_matches_the_header_signatures():
+    """Every ctypes signature has the header's parameter count and kinds, so a call
+    with a wrong argument list fails in Python instead of reading garbage."""
+    kinds = {ctypes.c_void_p: "p", ctypes.c_char_p: "p", ctypes.c_int64: "i64", ctypes.c_int: "i"}
+    declared = _declarations()
+    assert sorted(declared) == sorted(_lib.EXPORTED_SYMBOLS)
+    for name, (restype, argtypes) in _lib._SIGNATURES.items():
+        ret, params = declared[name]
+        assert [kinds[t] for t in argtypes] == params, name
+        assert kinds[restype] == ret, name
+
+
 def test_library_exports_every_declared_symbol():
     lib = _lib.load_library()
     handle = ctypes.CDLL(str(lib.path))
